@@ -1,0 +1,166 @@
+/*
+ * lk_attn.h - C ABI of the MI355X (gfx950) attention hot path of the
+ * lfm2-ampere engine: split-K GQA decode attention over the fp16 KV cache with
+ * a deterministic two-stage combine, and chunked causal prefill attention with
+ * int8 Q.K^T scoring, exact fp16 tiles at the diagonal window and the sink,
+ * online softmax and fp16 P.V.
+ *
+ * Conventions (the reference engine's, /root/reference/src/engine.cu:21-22,
+ * 397-409, 974-985):
+ *   - every buffer is caller-owned DEVICE memory; no entry point allocates,
+ *     frees or synchronises.  Each one only enqueues work on `stream`
+ *     (a hipStream_t passed as void*; NULL = the default stream);
+ *   - the decode sequence length is read ON THE DEVICE from d_pos
+ *     (seq = *d_pos + 1) and the grids are fixed, so the decode launches are
+ *     position-independent and may be captured into a hipGraph;
+ *   - every entry point returns 0 (hipSuccess) or a hipError_t code; argument
+ *     errors the host can see return hipErrorInvalidValue (1) and launch
+ *     nothing.  lk_last_error() describes the last failure in words.
+ *
+ * Model constants (reference kernels.cuh:12-24): 32 query heads, 8 KV heads
+ * (GQA 4:1), head_dim 64, softmax scale 1/8.  The KV cache of one layer is
+ * fp16 [max_seq][8][64].
+ */
+#ifndef LK_ATTN_H
+#define LK_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LK_N_HEADS      32
+#define LK_N_KV_HEADS   8
+#define LK_HEAD_DIM     64
+#define LK_ATTN_PARTW   (2 + LK_HEAD_DIM)   /* partial record: m, l, acc[64] */
+
+/* Q8_1 activation block (reference quant.cuh:27-31): fp16 d = amax/127 and
+ * fp16 raw sum of the 32 values, then the 32 int8 quants.  36 bytes. */
+typedef struct lk_block_q8_1 {
+    uint16_t d;      /* fp16 bits */
+    uint16_t s;      /* fp16 bits */
+    int8_t   qs[32];
+} lk_block_q8_1;
+
+/* ---- build-time configuration ------------------------------------------- */
+
+/* The split-K operating point this library was built with: the slice count is
+ * clamp(ceil(seq / target_n), split_min, split_cap)
+ * (reference kernels.cuh:630-635, retuned for 256 CUs). */
+int lk_attn_config(int * split_cap, int * target_n, int * split_min);
+
+/* Bytes the caller must allocate for `part` (fp32 [32][split_cap][66]).
+ * Replaces the engine's own sizing at reference engine.cu:408-409. */
+size_t lk_attn_part_bytes(void);
+
+/* Human-readable description of the last error returned on this thread. */
+const char * lk_last_error(void);
+
+/* ---- decode attention ----------------------------------------------------
+ * q   : fp32 [32][64], post-RoPE
+ * kc  : fp16 [max_seq][8][64] K cache of this layer
+ * vc  : fp16 [max_seq][8][64] V cache of this layer
+ * d_pos: int32, device; the kernels attend to positions [0, *d_pos]
+ * part: fp32 scratch of lk_attn_part_bytes() bytes
+ * out : fp32 [32][64] or NULL
+ * yq8 : lk_block_q8_1 [64] (two blocks per head) or NULL
+ */
+
+/* Replaces k_attn_split (reference kernels.cuh:647-649, kernels.cu:1303-1556).
+ * Grid (8 kv heads x split_cap), blocks past the live slice count exit. */
+int lk_attn_split(const float * q, const void * kc, const void * vc,
+                  const int * d_pos, float * part, void * stream);
+
+/* Replaces k_attn_combine (reference kernels.cuh:650-652, kernels.cu:1558-1599).
+ * Slice partials are merged in a fixed order, so output is run-to-run
+ * bit-identical. */
+int lk_attn_combine(const float * part, const int * d_pos, float * out,
+                    lk_block_q8_1 * yq8, void * stream);
+
+/* lk_attn_split followed by lk_attn_combine: the two graph nodes the engine
+ * launches per attention layer (reference engine.cu:638-641). */
+int lk_attn_decode(const float * q, const void * kc, const void * vc,
+                   const int * d_pos, float * part, float * out,
+                   lk_block_q8_1 * yq8, void * stream);
+
+/* Replaces k_attention_decode (reference kernels.cuh:653-658,
+ * kernels.cu:768-852): one workgroup per query head, a cross-check only.
+ * Like the reference it only serves seq <= 8192; for longer sequences it
+ * writes nothing (the reference prints FATAL and returns). */
+#define LK_ATTN_DECODE_MAX_SEQ 8192
+int lk_attention_decode(const float * q, const void * kc, const void * vc,
+                        const int * d_pos, float * out, lk_block_q8_1 * yq8,
+                        void * stream);
+
+/* ---- decode graph --------------------------------------------------------
+ * The engine captures its whole decode step once and replays it
+ * (reference engine.cu:1333-1343); these capture just the attention slice:
+ * n_layers x (split, combine) on one stream, into one hipGraph.  The arrays
+ * hold one pointer per layer; `part` is shared by all layers (the layers run
+ * in stream order).  out[i] / yq8[i] may be NULL, and so may the arrays. */
+typedef struct lk_decode_graph lk_decode_graph;
+int lk_decode_graph_create(int n_layers, const float * const * q,
+                           const void * const * kc, const void * const * vc,
+                           const int * d_pos, float * part,
+                           float * const * out, lk_block_q8_1 * const * yq8,
+                           void * stream, lk_decode_graph ** graph);
+int lk_decode_graph_launch(lk_decode_graph * graph, void * stream);
+int lk_decode_graph_nodes(const lk_decode_graph * graph, size_t * n_nodes);
+int lk_decode_graph_destroy(lk_decode_graph * graph);
+
+/* ---- prefill: int8 quantisers ---------------------------------------------
+ * Per (row, head) 64-wide absmax quantisation (reference prefill.cu:1255-1267):
+ * d = amax/127, q = rint(v * (127/amax)), scale = d * mul.  Bit-exact. */
+
+/* Replaces k_pf_q8 (reference prefill.cuh:98-99, prefill.cu:1271-1287).
+ * qh : fp16 [m][2048] (already x 1/8)  ->  q8 int8 [m][2048],
+ * qsc fp32 [m][32] = d * log2(e), qcs fp32 [m][32] = (q.c) * log2(e) when
+ * cm != NULL else 0.  cm: fp32 [8][64] smoothing vector or NULL. */
+int lk_pf_q8(const void * qh, int m, const float * cm, int8_t * q8,
+             float * qsc, float * qcs, void * stream);
+
+/* Replaces k_pf_k8 (reference prefill.cuh:100-101, prefill.cu:1291-1301).
+ * Positions [p0, p1) of kc fp16 [pos][8][64] -> k8 int8 (same layout) and
+ * ksc fp32 [8][kstride] (head-major).  kstride must be a multiple of 4 and
+ * >= p1.  cm as above. */
+int lk_pf_k8(const void * kc, int p0, int p1, const float * cm, int kstride,
+             int8_t * k8, float * ksc, void * stream);
+
+/* Replaces k_pf_kmean (reference prefill.cuh:102, prefill.cu:1304-1318):
+ * cm[h][d] = mean over positions [0, n) of kc.  Fixed summation order. */
+int lk_pf_kmean(const void * kc, int n, float * cm, void * stream);
+
+/* ---- prefill attention -----------------------------------------------------
+ * One causal chunk of m query positions starting at position P, attending to
+ * key positions [0, P + m).  o: fp32 [m][2048] (row = query, col = head*64+d).
+ */
+
+/* Replaces k_pf_attn8 (reference prefill.cuh:105-109, prefill.cu:1337-1571).
+ * Key tiles of 64 within `near` positions of a 32-query tile's first query,
+ * and key tile 0 when `sink` != 0, are scored exactly in fp16; all others use
+ * int8 Q.K^T with int32 sums. */
+int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * qcs,
+                const void * qh, int m, int P, const int8_t * k8,
+                const float * ksc, int kstride, const void * kc,
+                const void * vc, int near, int sink, float * o, void * stream);
+
+/* Replaces k_pf_attn (reference prefill.cuh:94-96, prefill.cu:1029-1226):
+ * the same attention with every tile exact fp16. */
+int lk_pf_attn(const void * qh, int m, int P, const void * kc, const void * vc,
+               float * o, void * stream);
+
+/* ---- test hook --------------------------------------------------------------
+ * The raw int32 Q.K^T sums of the int8 scoring path, computed by the same
+ * matrix-core routine lk_pf_attn8 uses:  s[head][i][j] = sum_d q8[i][head][d] *
+ * k8[j][head/4][d] for i < m, j < n  (s: int32 [32][m][n]).  m and n must be
+ * multiples of 16.  No counterpart in the reference; exists so the int32 sums
+ * can be checked bit-exactly. */
+int lk_pf_qk_i32(const int8_t * q8, int m, const int8_t * k8, int n,
+                 int32_t * s, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LK_ATTN_H */

@@ -1,0 +1,219 @@
+"""Python host mirror of the attention entry points (ctypes over liblk_attn.so).
+
+The reference engine is C++ and launches its attention kernels directly
+(/root/reference/src/engine.cu:638-641 for decode, :1082-1089 and :1122 for
+prefill).  This module binds the C ABI of ``include/lk_attn.h`` under the
+reference's kernel names (``attn_split`` for ``k_attn_split`` and so on) so
+tests and the benchmark read like the reference's own harnesses.  PyTorch is
+used only to own device memory and streams; every computation runs in the HIP
+library.  There is no fallback: if the library is missing or fails, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblk_attn.so")
+
+N_HEADS, N_KV_HEADS, HEAD_DIM = 32, 8, 64
+PARTW = 2 + HEAD_DIM
+DECODE_MAX_SEQ = 8192
+Q8_1_BYTES = 36
+
+# Every symbol the header declares; tests check the library exports them all.
+EXPORTS = (
+    "lk_attn_config", "lk_attn_part_bytes", "lk_last_error",
+    "lk_attn_split", "lk_attn_combine", "lk_attn_decode", "lk_attention_decode",
+    "lk_decode_graph_create", "lk_decode_graph_launch", "lk_decode_graph_nodes",
+    "lk_decode_graph_destroy",
+    "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_qk_i32",
+)
+
+
+class LkError(RuntimeError):
+    """A C-ABI call returned a non-zero hipError_t."""
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load liblk_attn.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise FileNotFoundError(
+            f"{path} is missing: build it with `make -C lfm2-ampere_amd` "
+            "(or __graft_entry__.build()); there is no fallback path")
+    lib = ctypes.CDLL(path)
+    P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    sig = {
+        "lk_attn_config": ([P, P, P], I),
+        "lk_attn_part_bytes": ([], S),
+        "lk_last_error": ([], ctypes.c_char_p),
+        "lk_attn_split": ([P, P, P, P, P, P], I),
+        "lk_attn_combine": ([P, P, P, P, P], I),
+        "lk_attn_decode": ([P, P, P, P, P, P, P, P], I),
+        "lk_attention_decode": ([P, P, P, P, P, P, P], I),
+        "lk_decode_graph_create": ([I, P, P, P, P, P, P, P, P, P], I),
+        "lk_decode_graph_launch": ([P, P], I),
+        "lk_decode_graph_nodes": ([P, P], I),
+        "lk_decode_graph_destroy": ([P], I),
+        "lk_pf_q8": ([P, I, P, P, P, P, P], I),
+        "lk_pf_k8": ([P, I, I, P, I, P, P, P], I),
+        "lk_pf_kmean": ([P, I, P, P], I),
+        "lk_pf_attn8": ([P, P, P, P, I, I, P, P, I, P, P, I, I, P, P], I),
+        "lk_pf_attn": ([P, I, I, P, P, P, P], I),
+        "lk_pf_qk_i32": ([P, I, P, I, P, P], I),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().lk_last_error().decode(errors="replace")
+        raise LkError(f"{what} failed (hipError {rc}): {msg}")
+
+
+def _ptr(t) -> Optional[int]:
+    """Device pointer of a tensor (None -> NULL).  Checks residency and layout."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("lk_attn: tensors must live in device memory")
+    if not t.is_contiguous():
+        raise ValueError("lk_attn: tensors must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(stream) -> Optional[int]:
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream or None
+
+
+def config() -> dict:
+    a, b, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _check(load().lk_attn_config(ctypes.byref(a), ctypes.byref(b), ctypes.byref(c)), "lk_attn_config")
+    return {"split_cap": a.value, "target_n": b.value, "split_min": c.value}
+
+
+def part_bytes() -> int:
+    return int(load().lk_attn_part_bytes())
+
+
+def attn_slices(seq: int) -> tuple:
+    """The library's split-K slice rule (reference kernels.cuh:630-635)."""
+    c = config()
+    s = (seq + c["target_n"] - 1) // c["target_n"]
+    s = max(c["split_min"], min(c["split_cap"], s))
+    return s, (seq + s - 1) // s
+
+
+# ---- decode (reference kernels.cuh:644-658) -------------------------------------
+def attn_split(q, kc, vc, d_pos, part, stream=None) -> None:
+    _check(load().lk_attn_split(_ptr(q), _ptr(kc), _ptr(vc), _ptr(d_pos), _ptr(part),
+                                _stream(stream)), "lk_attn_split")
+
+
+def attn_combine(part, d_pos, out=None, yq8=None, stream=None) -> None:
+    _check(load().lk_attn_combine(_ptr(part), _ptr(d_pos), _ptr(out), _ptr(yq8),
+                                  _stream(stream)), "lk_attn_combine")
+
+
+def attn_decode(q, kc, vc, d_pos, part, out=None, yq8=None, stream=None) -> None:
+    _check(load().lk_attn_decode(_ptr(q), _ptr(kc), _ptr(vc), _ptr(d_pos), _ptr(part),
+                                 _ptr(out), _ptr(yq8), _stream(stream)), "lk_attn_decode")
+
+
+def attention_decode(q, kc, vc, d_pos, out=None, yq8=None, stream=None) -> None:
+    _check(load().lk_attention_decode(_ptr(q), _ptr(kc), _ptr(vc), _ptr(d_pos), _ptr(out),
+                                      _ptr(yq8), _stream(stream)), "lk_attention_decode")
+
+
+class DecodeGraph:
+    """n_layers x (split, combine) captured into one hipGraph."""
+
+    def __init__(self, qs: Sequence, kcs: Sequence, vcs: Sequence, d_pos, part,
+                 outs: Optional[Sequence] = None, yq8s: Optional[Sequence] = None, stream=None):
+        import torch
+        n = len(qs)
+        if not (len(kcs) == n and len(vcs) == n):
+            raise ValueError("DecodeGraph: per-layer lists must have equal length")
+        arr = ctypes.c_void_p * n
+        self._keep = (qs, kcs, vcs, d_pos, part, outs, yq8s)
+        self._stream = stream if stream is not None else torch.cuda.Stream()
+        h = ctypes.c_void_p()
+        o = arr(*[_ptr(t) for t in outs]) if outs is not None else None
+        y = arr(*[_ptr(t) for t in yq8s]) if yq8s is not None else None
+        _check(load().lk_decode_graph_create(
+            n, arr(*[_ptr(t) for t in qs]), arr(*[_ptr(t) for t in kcs]),
+            arr(*[_ptr(t) for t in vcs]), _ptr(d_pos), _ptr(part), o, y,
+            self._stream.cuda_stream, ctypes.byref(h)), "lk_decode_graph_create")
+        self._h = h
+
+    @property
+    def stream(self):
+        return self._stream
+
+    def nodes(self) -> int:
+        n = ctypes.c_size_t()
+        _check(load().lk_decode_graph_nodes(self._h, ctypes.byref(n)), "lk_decode_graph_nodes")
+        return n.value
+
+    def launch(self) -> None:
+        _check(load().lk_decode_graph_launch(self._h, self._stream.cuda_stream), "lk_decode_graph_launch")
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().lk_decode_graph_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- prefill (reference prefill.cuh:85-109) -------------------------------------
+def pf_q8(qh, m, cm, q8, qsc, qcs, stream=None) -> None:
+    _check(load().lk_pf_q8(_ptr(qh), m, _ptr(cm), _ptr(q8), _ptr(qsc), _ptr(qcs), _stream(stream)),
+           "lk_pf_q8")
+
+
+def pf_k8(kc, p0, p1, cm, kstride, k8, ksc, stream=None) -> None:
+    _check(load().lk_pf_k8(_ptr(kc), p0, p1, _ptr(cm), kstride, _ptr(k8), _ptr(ksc), _stream(stream)),
+           "lk_pf_k8")
+
+
+def pf_kmean(kc, n, cm, stream=None) -> None:
+    _check(load().lk_pf_kmean(_ptr(kc), n, _ptr(cm), _stream(stream)), "lk_pf_kmean")
+
+
+def pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, stream=None) -> None:
+    _check(load().lk_pf_attn8(_ptr(q8), _ptr(qsc), _ptr(qcs), _ptr(qh), m, P, _ptr(k8), _ptr(ksc),
+                              kstride, _ptr(kc), _ptr(vc), near, sink, _ptr(o), _stream(stream)),
+           "lk_pf_attn8")
+
+
+def pf_attn(qh, m, P, kc, vc, o, stream=None) -> None:
+    _check(load().lk_pf_attn(_ptr(qh), m, P, _ptr(kc), _ptr(vc), _ptr(o), _stream(stream)), "lk_pf_attn")
+
+
+def pf_qk_i32(q8, m, k8, n, s, stream=None) -> None:
+    _check(load().lk_pf_qk_i32(_ptr(q8), m, _ptr(k8), n, _ptr(s), _stream(stream)), "lk_pf_qk_i32")
+
+
+def kstride_for(S: int) -> int:
+    """ksc row stride for S positions: rounded up to 4 (reference engine.cu:979)."""
+    return (S + 3) & ~3

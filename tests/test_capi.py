@@ -1,0 +1,77 @@
+"""The C-ABI library loads and exports every entry point include/lk_attn.h
+declares; host-side argument checks reject bad calls without launching.
+CPU only: no kernel is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "lk_attn.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(lk_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_and_binding_agree():
+    import lk_attn
+    assert _declared() == sorted(lk_attn.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    import lk_attn
+    lib = ctypes.CDLL(lk_attn.LIB_PATH)
+    missing = [s for s in _declared() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_config_and_part_size():
+    import lk_attn
+    c = lk_attn.config()
+    assert c["split_min"] >= 1 and c["target_n"] >= 16 and c["split_cap"] >= c["split_min"]
+    assert lk_attn.part_bytes() == 32 * c["split_cap"] * 66 * 4
+
+
+def test_slice_rule_binding_matches_oracle(oracle):
+    import lk_attn
+    c = lk_attn.config()
+    for seq in [1, 5, 100, 513, 4096, 32768, 100003, 131072]:
+        assert lk_attn.attn_slices(seq) == oracle.attn_slices(seq, c["split_cap"], c["target_n"], c["split_min"])
+
+
+def test_host_argument_errors():
+    import lk_attn
+    lib = lk_attn.load()
+    p = ctypes.c_void_p(0x1000)      # never dereferenced: every call below fails validation
+    assert lib.lk_attn_split(None, p, p, p, p, None) == 1
+    assert b"null" in lib.lk_last_error()
+    assert lib.lk_attn_combine(None, p, None, None, None) == 1
+    assert lib.lk_pf_k8(p, 0, 10, None, 6, p, p, None) == 1            # kstride not a multiple of 4
+    assert b"kstride" in lib.lk_last_error()
+    assert lib.lk_pf_k8(p, 5, 3, None, 8, p, p, None) == 1             # p1 < p0
+    assert lib.lk_pf_attn8(p, p, p, p, 10, 0, p, p, 8, p, p, 0, 0, p, None) == 1   # kstride < P+m
+    assert lib.lk_pf_qk_i32(p, 17, p, 16, p, None) == 1
+    assert lib.lk_pf_kmean(p, 0, p, None) == 1
+    # empty work is a successful no-op
+    assert lib.lk_pf_q8(None, 0, None, None, None, None, None) == 0
+    assert lib.lk_pf_attn(None, 0, 0, None, None, None, None) == 0
+    assert lib.lk_pf_k8(None, 4, 4, None, 8, None, None, None) == 0
+    h = ctypes.c_void_p()
+    assert lib.lk_decode_graph_create(0, None, None, None, None, None, None, None, p, ctypes.byref(h)) == 1
+    assert lib.lk_decode_graph_launch(None, None) == 1
+    assert lib.lk_decode_graph_destroy(None) == 0
+
+
+def test_python_mirror_fails_loudly_without_library(tmp_path):
+    import importlib
+    import lk_attn
+    mod = importlib.reload(lk_attn)
+    try:
+        mod._lib = None
+        with pytest.raises(FileNotFoundError):
+            mod.load(str(tmp_path / "missing.so"))
+    finally:
+        importlib.reload(lk_attn)

@@ -1,0 +1,211 @@
+"""Decode attention parity on the GPU, through the C ABI.
+
+Mirrors the reference's gate G6 (tests/test_attn.cu): the same xorshift64
+inputs (seed 0x9e3779b97f4a7c15, state carried from case to case, the whole
+131072-position cache filled per case), the same 12 lengths in the same order,
+split+combine and the serial kernel each against the float64 reference, and
+split against serial.  Tolerances: the reference's 1e-3 absolute (1e-4 split vs
+serial) and the north-star 2e-3 max relative error; the combine's Q8_1 output is
+checked bit-exactly.  Also: determinism, the hipGraph, the BASELINE decode
+configurations and the error paths.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import abs_err, d_pos_for, dev, dev_h, host, note
+
+pytestmark = pytest.mark.gpu
+
+REF_LENGTHS = [4096, 8192, 513, 512, 100, 5, 1, 16384, 32768, 65536, 100003, 131072]
+CACHE = 131072 * 8 * 64
+
+
+class _XsCases:
+    """Generates test_attn.cu's cases in order, carrying the generator state."""
+
+    def __init__(self, oracle):
+        self.gen = oracle.XorShiftAttnCases()
+        self.done = -1
+        self.data = None
+
+    def case(self, idx):
+        assert idx >= self.done, "cases must be requested in reference order"
+        while self.done < idx:
+            self.data = self.gen.next_case(CACHE)
+            self.done += 1
+        return self.data
+
+
+@pytest.fixture(scope="module")
+def xs_cases(oracle):
+    return _XsCases(oracle)
+
+
+def _run_decode(lk, q, kc, vc, seq, yq8=False):
+    d_pos = d_pos_for(seq)
+    part = torch.empty(lk.part_bytes() // 4, dtype=torch.float32, device="cuda")
+    out = torch.full((32, 64), float("nan"), device="cuda")
+    y = torch.zeros(64 * 36, dtype=torch.uint8, device="cuda") if yq8 else None
+    lk.attn_decode(q, kc, vc, d_pos, part, out, y)
+    torch.cuda.synchronize()
+    return out, y
+
+
+@pytest.mark.parametrize("idx", range(len(REF_LENGTHS)), ids=[f"seq{s}" for s in REF_LENGTHS])
+def test_reference_cases(lk, oracle, xs_cases, idx):
+    seq = REF_LENGTHS[idx]
+    q, kc, vc = xs_cases.case(idx)
+    note(f"decode reference case seq={seq}")
+    qd, kd, vd = dev(q), dev_h(kc), dev_h(vc)
+    out, y = _run_decode(lk, qd, kd, vd, seq, yq8=True)
+    ref = oracle.decode_ref(q, kc, vc, seq)
+    o = host(out)
+    ep = abs_err(o, ref)
+    rel = oracle.rel_err(o, ref)
+    note(f"  split vs float64: abs {ep:.3e} rel {rel:.3e}")
+    assert ep <= 1e-3 and rel <= 2e-3
+    # the combine's Q8_1 epilogue, bit-exact against the oracle on the same values
+    yb = host(y).reshape(64, 36)
+    for b in range(64):
+        assert np.array_equal(yb[b], oracle.quantize_q8_1(o.reshape(-1)[32 * b:32 * b + 32])), b
+    if seq <= lk.DECODE_MAX_SEQ:
+        os_ = torch.full((32, 64), float("nan"), device="cuda")
+        lk.attention_decode(qd, kd, vd, d_pos_for(seq), os_, None)
+        torch.cuda.synchronize()
+        os_ = host(os_)
+        es = abs_err(os_, ref)
+        note(f"  serial vs float64: abs {es:.3e}; split vs serial {abs_err(os_, o):.3e}")
+        assert es <= 1e-3 and abs_err(os_, o) <= 1e-4
+
+
+def test_seq1_is_v_exactly(lk, oracle):
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((32, 64)).astype(np.float32)
+    kc = rng.standard_normal((64, 8, 64)).astype(np.float16)
+    vc = rng.standard_normal((64, 8, 64)).astype(np.float16)
+    note("decode seq=1 closed form")
+    out, _ = _run_decode(lk, dev(q), dev_h(kc.view(np.uint16)), dev_h(vc.view(np.uint16)), 1)
+    assert np.array_equal(host(out), np.repeat(vc[0].astype(np.float32), 4, axis=0))
+
+
+def test_constant_keys_average(lk, oracle):
+    rng = np.random.default_rng(22)
+    seq = 3000
+    q = rng.standard_normal((32, 64)).astype(np.float32)
+    kc = np.ascontiguousarray(np.broadcast_to(rng.standard_normal((1, 8, 64)), (seq, 8, 64))).astype(np.float16)
+    vc = rng.standard_normal((seq, 8, 64)).astype(np.float16)
+    note("decode constant keys")
+    out, _ = _run_decode(lk, dev(q), dev_h(kc.view(np.uint16)), dev_h(vc.view(np.uint16)), seq)
+    want = np.repeat(vc.astype(np.float64).mean(0), 4, axis=0)
+    assert abs_err(host(out), want) <= 1e-5
+
+
+def test_bitwise_deterministic(lk, oracle):
+    rng = np.random.default_rng(23)
+    seq = 77777
+    q = rng.standard_normal((32, 64)).astype(np.float32)
+    kd = torch.randn(seq, 8, 64, device="cuda").half()
+    vd = torch.randn(seq, 8, 64, device="cuda").half()
+    note("decode determinism seq=77777")
+    outs = [host(_run_decode(lk, dev(q), kd, vd, seq, yq8=True)[0]) for _ in range(5)]
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
+def test_null_outputs_and_q8_only(lk, oracle):
+    rng = np.random.default_rng(24)
+    seq = 1000
+    q = dev(rng.standard_normal((32, 64)).astype(np.float32))
+    kd = torch.randn(seq, 8, 64, device="cuda").half()
+    vd = torch.randn(seq, 8, 64, device="cuda").half()
+    part = torch.empty(lk.part_bytes() // 4, device="cuda")
+    d_pos = d_pos_for(seq)
+    note("decode nullable outputs")
+    y1 = torch.zeros(64 * 36, dtype=torch.uint8, device="cuda")
+    lk.attn_decode(q, kd, vd, d_pos, part, None, y1)
+    out = torch.empty(32, 64, device="cuda")
+    y2 = torch.zeros(64 * 36, dtype=torch.uint8, device="cuda")
+    lk.attn_split(q, kd, vd, d_pos, part)
+    lk.attn_combine(part, d_pos, out, y2)
+    lk.attn_combine(part, d_pos, None, None)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
+def test_serial_beyond_limit_writes_nothing(lk):
+    seq = lk.DECODE_MAX_SEQ + 1
+    q = torch.randn(32, 64, device="cuda")
+    kd = torch.randn(seq, 8, 64, device="cuda").half()
+    out = torch.full((32, 64), 7.0, device="cuda")
+    note("serial decode beyond its limit")
+    lk.attention_decode(q, kd, kd, d_pos_for(seq), out, None)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+
+
+def test_graph_replay_matches_eager_and_is_position_independent(lk, oracle):
+    layers, cap = 10, 6000
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    qs = [torch.randn(32, 64, device="cuda", generator=g) for _ in range(layers)]
+    kcs = [torch.randn(cap, 8, 64, device="cuda", generator=g).half() for _ in range(layers)]
+    vcs = [torch.randn(cap, 8, 64, device="cuda", generator=g).half() for _ in range(layers)]
+    d_pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    part = torch.empty(lk.part_bytes() // 4, device="cuda")
+    outs = [torch.empty(32, 64, device="cuda") for _ in range(layers)]
+    yq8s = [torch.zeros(64 * 36, dtype=torch.uint8, device="cuda") for _ in range(layers)]
+    note("decode graph capture, 10 layers")
+    graph = lk.DecodeGraph(qs, kcs, vcs, d_pos, part, outs, yq8s)
+    assert graph.nodes() == 2 * layers
+    eager_part = torch.empty_like(part)
+    for seq in [1, 129, 4000, 5999, 4000]:
+        d_pos.fill_(seq - 1)
+        torch.cuda.synchronize()
+        graph.launch()
+        graph.stream.synchronize()
+        for i in range(layers):
+            o = torch.empty(32, 64, device="cuda")
+            y = torch.zeros(64 * 36, dtype=torch.uint8, device="cuda")
+            lk.attn_decode(qs[i], kcs[i], vcs[i], d_pos, eager_part, o, y)
+            torch.cuda.synchronize()
+            assert torch.equal(o.view(torch.int32), outs[i].view(torch.int32)), (seq, i)
+            assert torch.equal(y, yq8s[i]), (seq, i)
+        kh = kcs[3][:seq].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        vh = vcs[3][:seq].contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+        ref = oracle.decode_ref(host(qs[3]), kh, vh, seq)
+        assert oracle.rel_err(host(outs[3]), ref) <= 2e-3
+    graph.close()
+
+
+def _check_config(lk, oracle, cfg, layers, check_layers):
+    import lk_configs
+    note(f"decode config {cfg} ({layers} layer(s))")
+    qs, kcs, vcs, seq = lk_configs.decode_inputs(cfg, layers=layers)
+    d_pos = d_pos_for(seq)
+    part = torch.empty(lk.part_bytes() // 4, device="cuda")
+    outs = [torch.empty(32, 64, device="cuda") for _ in range(layers)]
+    graph = lk.DecodeGraph(qs, kcs, vcs, d_pos, part, outs)
+    graph.launch()
+    graph.stream.synchronize()
+    for i in check_layers:
+        kh = kcs[i].view(torch.int16).cpu().numpy().view(np.uint16)
+        vh = vcs[i].view(torch.int16).cpu().numpy().view(np.uint16)
+        ref = oracle.decode_ref(host(qs[i]), kh, vh, seq)
+        o = host(outs[i])
+        rel = oracle.rel_err(o, ref)
+        note(f"  layer {i}: abs {abs_err(o, ref):.3e} rel {rel:.3e}")
+        assert rel <= 2e-3 and abs_err(o, ref) <= 1e-3
+    graph.close()
+
+
+def test_config_c1(lk, oracle):
+    _check_config(lk, oracle, "C1", 1, [0])
+
+
+def test_config_c2(lk, oracle):
+    _check_config(lk, oracle, "C2", 1, [0])
+
+
+def test_config_c3_graph(lk, oracle):
+    _check_config(lk, oracle, "C3", 10, [0, 9])

@@ -1,0 +1,376 @@
+"""Pins of the CPU oracle (oracle/lk_oracle.cpp) -- CPU only.
+
+The reference holds no attention golden vectors (its attention tests are
+seeded-random float64 comparisons), so each oracle function is pinned against
+something that is not itself: a library routine (numpy's IEEE fp16 conversion,
+torch's float64 scaled_dot_product_attention, numpy integer matmul), a closed
+form (seq = 1, constant keys, the lossless int8 grid the reference's own
+test_attn8 relies on, tie-breaking of the two rounding rules), numbers printed
+in the reference's sources, or a published test vector.  Each check is chosen
+so that a plausible slip (wrong rounding rule, dropped scale, transposed
+operand, wrong GQA head mapping, off-by-one tile boundary) fails it.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+
+# ---- fp16 conversions -----------------------------------------------------------
+def test_h2f_exhaustive(oracle):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = h.view(np.float16).astype(np.float32)
+    got = oracle.h2f(h)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f2h_matches_numpy_rne(oracle):
+    rng = np.random.default_rng(7)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 200000),
+        # exact ties between neighbouring halves (normal and subnormal), overflow edge
+        (np.arange(1, 4000, dtype=np.float32) + 0.5) * np.float32(2.0 ** -10),
+        (np.arange(0, 2000, dtype=np.float32) + 0.5) * np.float32(2.0 ** -24),
+        np.array([65504, 65519.99, 65520, 70000, -65520, 6.1e-5, 5.96e-8, 2.98e-8,
+                  2.99e-8, 0.0, -0.0, np.inf, -np.inf], np.float32),
+    ]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    got = oracle.f2h(x)
+    assert np.array_equal(got, ref)
+
+
+# ---- split-K slice rule -------------------------------------------------------------
+@pytest.mark.parametrize("seq,ns,chunk", [
+    # the reference operating point SPLIT=128, TARGET_N=64, SPLIT_MIN=8 and the
+    # chunk sizes its sources state (test_attn.cu:224-228, kernels.cuh:623-625)
+    (16384, 128, 128), (32768, 128, 256), (65536, 128, 512), (100003, 128, 782),
+    (131072, 128, 1024), (4096, 64, 64), (8192, 128, 64), (1, 8, 1), (5, 8, 1),
+])
+def test_slice_rule_reference_points(oracle, seq, ns, chunk):
+    assert oracle.attn_slices(seq, 128, 64, 8) == (ns, chunk)
+
+
+def test_slice_rule_covers_sequence(oracle):
+    for cap, tn, mn in [(128, 64, 8), (256, 128, 8), (512, 256, 16)]:
+        for seq in [1, 2, 7, 63, 64, 65, 511, 4097, 32768, 100003, 131072]:
+            ns, ch = oracle.attn_slices(seq, cap, tn, mn)
+            assert mn <= ns <= cap and ch * ns >= seq and ch * (ns - 1) < seq or ns == mn
+            nv = -(-seq // ch)
+            assert nv <= ns and (nv - 1) * ch < seq <= nv * ch
+
+
+# ---- decode float64 reference ----------------------------------------------------------
+def _rand_kv(rng, seq):
+    k = rng.uniform(-1, 1, (seq, 8, 64)).astype(np.float16)
+    v = rng.uniform(-1, 1, (seq, 8, 64)).astype(np.float16)
+    return k, v
+
+
+def test_decode_ref_seq1_is_v(oracle):
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((32, 64)).astype(np.float32)
+    k, v = _rand_kv(rng, 1)
+    out = oracle.decode_ref(q, k.view(np.uint16), v.view(np.uint16), 1)
+    want = np.repeat(v[0].astype(np.float64), 4, axis=0)       # head h uses kv h // 4
+    assert np.array_equal(out, want)
+
+
+def test_decode_ref_constant_keys_average_v(oracle):
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((32, 64)).astype(np.float32)
+    seq = 37
+    k = np.broadcast_to(rng.uniform(-1, 1, (1, 8, 64)), (seq, 8, 64)).astype(np.float16)
+    v = rng.uniform(-1, 1, (seq, 8, 64)).astype(np.float16)
+    out = oracle.decode_ref(q, np.ascontiguousarray(k).view(np.uint16), v.view(np.uint16), seq)
+    want = np.repeat(v.astype(np.float64).mean(0), 4, axis=0)
+    np.testing.assert_allclose(out, want, rtol=0, atol=1e-14)
+
+
+def test_decode_ref_matches_torch_sdpa(oracle):
+    rng = np.random.default_rng(3)
+    seq = 301
+    q = (rng.standard_normal((32, 64)) * 1.5).astype(np.float32)
+    k, v = _rand_kv(rng, seq)
+    out = oracle.decode_ref(q, k.view(np.uint16), v.view(np.uint16), seq)
+    qt = torch.from_numpy(q.astype(np.float64)).view(1, 32, 1, 64)
+    kt = torch.from_numpy(k.astype(np.float64)).permute(1, 0, 2).repeat_interleave(4, 0)[None]
+    vt = torch.from_numpy(v.astype(np.float64)).permute(1, 0, 2).repeat_interleave(4, 0)[None]
+    ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, scale=0.125)
+    np.testing.assert_allclose(out, ref.view(32, 64).numpy(), rtol=0, atol=1e-13)
+
+
+# ---- Q8_1 (combine epilogue) ---------------------------------------------------------------
+def _unpack_q8_1(y):
+    d = np.frombuffer(y[:2].tobytes(), np.float16)[0]
+    s = np.frombuffer(y[2:4].tobytes(), np.float16)[0]
+    return float(d), float(s), y[4:].view(np.int8).copy()
+
+
+def test_q8_1_zero_block(oracle):
+    d, s, q = _unpack_q8_1(oracle.quantize_q8_1(np.zeros(32, np.float32)))
+    assert d == 0.0 and s == 0.0 and not q.any()
+
+
+def test_q8_1_integer_grid_and_sum(oracle):
+    rng = np.random.default_rng(4)
+    k = rng.integers(-127, 128, 32)
+    k[5] = -127                       # |max| = 127 -> d = 1 exactly
+    d, s, q = _unpack_q8_1(oracle.quantize_q8_1(k.astype(np.float32)))
+    assert d == float(np.float16(np.float32(127.0) / np.float32(127.0)))
+    assert np.array_equal(q, k.astype(np.int8))
+    assert s == float(np.float16(k.sum()))      # small integers: the sum is exact in any order
+
+
+def test_q8_1_rounds_half_away_from_zero(oracle):
+    # am = 127 -> d = 1, so q = roundf(x): halves go AWAY from zero (roundf),
+    # unlike the prefill quantiser's round-to-nearest-even.
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:7] = [0.5, 1.5, 2.5, -0.5, -2.5, 126.5]
+    _, _, q = _unpack_q8_1(oracle.quantize_q8_1(x))
+    assert list(q[:7]) == [127, 1, 2, 3, -1, -3, 127]
+
+
+def test_q8_1_error_bound(oracle):
+    rng = np.random.default_rng(5)
+    for _ in range(200):
+        x = (rng.standard_normal(32) * 10.0 ** rng.uniform(-3, 3)).astype(np.float32)
+        d, s, q = _unpack_q8_1(oracle.quantize_q8_1(x))
+        dd = np.float32(np.abs(x).max()) / np.float32(127.0)
+        assert np.all(np.abs(q.astype(np.int32)) <= 127)
+        assert np.all(np.abs(x - q * dd) <= dd * (0.5 + 1e-5))
+        assert abs(s - x.astype(np.float64).sum()) <= 1e-3 * (abs(x).sum() + 1)
+
+
+# ---- prefill int8 quantiser ------------------------------------------------------------------
+def test_q8_row_lossless_grid(oracle):
+    # reference test_prefill.cu:301-309: integers with |max| = 127 times a power
+    # of two quantise losslessly.
+    rng = np.random.default_rng(6)
+    for j in range(-12, 6):
+        k = rng.integers(-127, 128, 64)
+        k[0] = 127
+        v = (k * 2.0 ** j).astype(np.float32)
+        q, sc = oracle.q8_row(v, mul=1.0)
+        assert np.array_equal(q, k.astype(np.int8))
+        assert sc == np.float32(np.float32(127 * 2.0 ** j) / np.float32(127.0))
+
+
+def test_q8_row_ties_to_even(oracle):
+    v = np.zeros(64, np.float32)
+    v[0] = 127.0                                   # id = 1 exactly
+    v[1:9] = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 125.5, 126.5]
+    q, sc = oracle.q8_row(v, mul=2.0)
+    assert list(q[:9]) == [127, 0, 2, 2, 0, -2, -2, 126, 126]
+    assert sc == np.float32(2.0)
+
+
+def test_q8_row_zero_and_bound(oracle):
+    q, sc = oracle.q8_row(np.zeros(64, np.float32))
+    assert not q.any() and sc == 0.0
+    rng = np.random.default_rng(8)
+    for _ in range(300):
+        v = (rng.standard_t(4, 64) * 10.0 ** rng.uniform(-4, 3)).astype(np.float32)
+        q, sc = oracle.q8_row(v)
+        assert np.abs(q.astype(np.int32)).max() == 127          # the max element maps to +-127
+        assert np.all(np.abs(v - q * sc) <= sc * 0.5 * (1 + 1e-5))
+
+
+def test_pf_q8_layout_and_scales(oracle):
+    rng = np.random.default_rng(9)
+    m = 3
+    qh = (rng.standard_normal((m, 2048)) * 0.2).astype(np.float16)
+    cm = rng.standard_normal((8, 64)).astype(np.float32)
+    q8, qsc, qcs = oracle.pf_q8(qh.view(np.uint16), m, cm)
+    q8n, qscn, qcsn = oracle.pf_q8(qh.view(np.uint16), m, None)
+    assert np.array_equal(q8, q8n) and np.array_equal(qsc, qscn) and not qcsn.any()
+    l2e = np.float32(1.4426950408889634)
+    for t in range(m):
+        for h in range(32):
+            row = qh[t, h * 64:(h + 1) * 64].astype(np.float32)
+            q, sc = oracle.q8_row(row, mul=float(l2e))
+            assert np.array_equal(q8[t, h * 64:(h + 1) * 64], q) and qsc[t, h] == sc
+            want = row.astype(np.float64) @ cm[h // 4].astype(np.float64) * float(l2e)
+            assert abs(qcs[t, h] - want) <= 1e-5 * (1 + abs(want))
+
+
+def test_pf_k8_layout_and_smoothing(oracle):
+    rng = np.random.default_rng(10)
+    S, kstride = 13, 16
+    kc = (rng.standard_normal((S, 8, 64)) * 1.5).astype(np.float16)
+    cm = rng.standard_normal((8, 64)).astype(np.float32) * 0.3
+    k8, ksc = oracle.pf_k8(kc.view(np.uint16), 3, 11, kstride, cm)
+    k8 = k8.reshape(S, 8, 64)
+    ksc = ksc.reshape(8, kstride)
+    assert not k8[:3].any() and not k8[11:].any() and not ksc[:, :3].any() and not ksc[:, 11:].any()
+    for p in range(3, 11):
+        for h in range(8):
+            q, sc = oracle.q8_row(kc[p, h].astype(np.float32) - cm[h])
+            assert np.array_equal(k8[p, h], q) and ksc[h, p] == sc
+
+
+def test_pf_kmean(oracle):
+    rng = np.random.default_rng(11)
+    n = 512
+    # small integers: every fp32 partial sum is exact, and n is a power of two,
+    # so the mean is exact whatever the summation order
+    kc = rng.integers(-40, 41, (n, 8, 64)).astype(np.float16)
+    cm = oracle.pf_kmean(kc.view(np.uint16), n)
+    assert np.array_equal(cm, kc.astype(np.float64).mean(0).astype(np.float32))
+    kc2 = rng.standard_normal((1000, 8, 64)).astype(np.float16)
+    cm2 = oracle.pf_kmean(kc2.view(np.uint16), 777)
+    np.testing.assert_allclose(cm2, kc2[:777].astype(np.float64).mean(0), rtol=0, atol=1e-6)
+
+
+# ---- exact-tile predicate -------------------------------------------------------------------
+def test_exact_tile_predicate(oracle):
+    # near covering the context: every tile exact (test_prefill.cu:857-858)
+    for P, m in [(150, 100), (1000, 37)]:
+        for qt in range((m + 31) // 32):
+            for kt in range((P + m + 63) // 64):
+                assert oracle.pf_exact(P, qt, kt, 1 << 20, 1)
+    # near = 0, no sink: exact iff the tile ends after the 32-query tile's first
+    # position, i.e. exactly the tiles that touch the diagonal region
+    P = 1000
+    for qt in range(2):
+        first = P + 32 * qt
+        for kt in range(20):
+            assert oracle.pf_exact(P, qt, kt, 0, 0) == (64 * kt + 63 >= first)
+    # sink keeps tile 0 exact; near widens the window by exactly `near` keys
+    assert oracle.pf_exact(4096, 5, 0, 0, 1) and not oracle.pf_exact(4096, 5, 0, 0, 0)
+    P, qt, near = 8192, 3, 1024
+    lo = P + 32 * qt - near
+    for kt in range(200):
+        assert oracle.pf_exact(P, qt, kt, near, 0) == (64 * kt + 64 > lo)
+
+
+# ---- prefill references -----------------------------------------------------------------------
+def _torch_causal(qh, kc, vc, m, P):
+    q = torch.from_numpy(qh.astype(np.float64)).view(m, 32, 64).permute(1, 0, 2)[None]
+    S = P + m
+    k = torch.from_numpy(kc.astype(np.float64)).view(S, 8, 64).permute(1, 0, 2).repeat_interleave(4, 0)[None]
+    v = torch.from_numpy(vc.astype(np.float64)).view(S, 8, 64).permute(1, 0, 2).repeat_interleave(4, 0)[None]
+    mask = torch.arange(S)[None, :] <= (P + torch.arange(m))[:, None]
+    o = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=1.0)
+    return o[0].permute(1, 0, 2).reshape(m, 2048).numpy()
+
+
+@pytest.mark.parametrize("m,P", [(5, 0), (37, 20), (64, 70)])
+def test_pf_ref_matches_torch_sdpa(oracle, m, P):
+    K, V, Q = oracle.mt_prefill_case(12345, m, P)
+    o = oracle.pf_ref(Q, m, P, K, V)
+    ref = _torch_causal(Q.view(np.float16), K.view(np.float16), V.view(np.float16), m, P)
+    np.testing.assert_allclose(o, ref, rtol=0, atol=1e-12)
+
+
+def _ref8_inputs(oracle, m, P, koff, with_off, smooth):
+    K, V, Q = oracle.mt_prefill_case(12345, m, P, koff, with_off)
+    S = P + m
+    kstride = (S + 3) & ~3
+    cm = oracle.pf_kmean(K, S) if smooth else None
+    q8, qsc, qcs = oracle.pf_q8(Q, m, cm)
+    k8, ksc = oracle.pf_k8(K, 0, S, kstride, cm)
+    return K, V, Q, q8, qsc, qcs, k8, ksc, kstride
+
+
+def test_pf_ref8_all_exact_equals_pf_ref(oracle):
+    m, P = 40, 90
+    K, V, Q, q8, qsc, qcs, k8, ksc, ks = _ref8_inputs(oracle, m, P, 3.0, True, True)
+    o8 = oracle.pf_ref8(q8, qsc, qcs, Q, m, P, k8, ksc, ks, K, V, 1 << 20, 1)
+    o = oracle.pf_ref(Q, m, P, K, V)
+    # the q.c shift cancels; what remains is the fp32 log2(e) constant
+    # (1.3e-8 relative) scaling the scores
+    np.testing.assert_allclose(o8, o, rtol=0, atol=1e-6)
+
+
+def test_pf_ref8_lossless_grid_int8_equals_exact(oracle):
+    # lossless int8 grid (test_prefill.cu:301-309): every int8 tile scores exactly
+    # what the fp16 tile would, so near = 0 must reproduce pf_ref.
+    m, P = 50, 100
+    K, V, Q, q8, qsc, qcs, k8, ksc, ks = _ref8_inputs(oracle, m, P, -1.0, True, False)
+    o8 = oracle.pf_ref8(q8, qsc, qcs, Q, m, P, k8, ksc, ks, K, V, 0, 0)
+    o = oracle.pf_ref(Q, m, P, K, V)
+    np.testing.assert_allclose(o8, o, rtol=0, atol=1e-6)
+
+
+def test_pf_ref8_int8_tiles_really_use_int8(oracle):
+    # On random data the int8 tiles must differ from exact scoring (else the
+    # classification is not being applied), and the tile-0 sink must matter.
+    m, P = 32, 320
+    K, V, Q, q8, qsc, qcs, k8, ksc, ks = _ref8_inputs(oracle, m, P, 0.0, True, False)
+    o = oracle.pf_ref(Q, m, P, K, V)
+    e_int8 = np.abs(oracle.pf_ref8(q8, qsc, qcs, Q, m, P, k8, ksc, ks, K, V, 0, 0) - o).max()
+    e_sink = np.abs(oracle.pf_ref8(q8, qsc, qcs, Q, m, P, k8, ksc, ks, K, V, 0, 1) - o).max()
+    e_all = np.abs(oracle.pf_ref8(q8, qsc, qcs, Q, m, P, k8, ksc, ks, K, V, 1 << 20, 0) - o).max()
+    assert e_all < 1e-6 and e_int8 > 1e-4 and e_sink > 0 and e_sink != e_int8
+
+
+def test_pf_ref8_int8_tile_formula(oracle):
+    # one query, one key, int8 tile: s = sumi * ksc * qsc, a one-key softmax
+    # returns V exactly; two keys give the closed-form two-way softmax.
+    m, P = 1, 1
+    K, V, Q, q8, qsc, qcs, k8, ksc, ks = _ref8_inputs(oracle, m, P, 0.0, True, False)
+    o = oracle.pf_ref8(q8, qsc, qcs, Q, m, P, k8, ksc, ks, K, V, -1000, 0)   # no exact tiles
+    Kq = k8.reshape(2, 8, 64).astype(np.int64)
+    Vf = V.view(np.float16).reshape(2, 8, 64).astype(np.float64)
+    for h in range(32):
+        s = [float((q8[0, h * 64:(h + 1) * 64].astype(np.int64) * Kq[j, h // 4]).sum())
+             * float(ksc[(h // 4) * ks + j]) * float(qsc[0, h]) for j in range(2)]
+        w = np.exp2(np.array(s) - max(s))
+        want = (w[:, None] * Vf[:, h // 4]).sum(0) / w.sum()
+        np.testing.assert_allclose(o[0, h * 64:(h + 1) * 64], want, rtol=0, atol=1e-12)
+
+
+def test_qk_i32_matches_integer_matmul(oracle):
+    rng = np.random.default_rng(12)
+    m, n = 16, 32
+    q8 = rng.integers(-127, 128, (m, 2048)).astype(np.int8)
+    k8 = rng.integers(-127, 128, (n, 8, 64)).astype(np.int8)
+    s = oracle.qk_i32(q8, m, k8, n)
+    qv = q8.reshape(m, 32, 64).astype(np.int64)
+    kv = np.repeat(k8.astype(np.int64), 4, axis=1)           # head h -> kv h // 4
+    want = np.einsum("ihd,jhd->hij", qv, kv)
+    assert np.array_equal(s, want.astype(np.int32))
+
+
+# ---- generators ---------------------------------------------------------------------------------
+def test_xorshift_generator_matches_definition(oracle):
+    # test_attn.cu:35-40: xorshift64 (13, 7, 17), top 53 bits / 2^53, then *2-1
+    gen = oracle.XorShiftAttnCases()
+    q, kc, vc = gen.next_case(cache_elems=4)
+    s = oracle.XorShiftAttnCases.SEED
+    M = (1 << 64) - 1
+
+    def nxt(s):
+        s ^= (s << 13) & M
+        s ^= s >> 7
+        s ^= (s << 17) & M
+        return s
+    vals = []
+    for _ in range(2048 + 8):
+        s = nxt(s)
+        vals.append(((s >> 11) & ((1 << 53) - 1)) / float(1 << 53) * 2.0 - 1.0)
+    assert np.array_equal(q, (np.array(vals[:2048], np.float32) * np.float32(1.5)))
+    kv = np.array(vals[2048:], np.float32).astype(np.float16).view(np.uint16)
+    assert np.array_equal(kc, kv[0::2]) and np.array_equal(vc, kv[1::2])
+    assert gen.state.value == s
+
+
+def test_splitmix_normal_stats(oracle):
+    x = oracle.sm_normal(42, 400000).astype(np.float64)
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
+    u = oracle.sm_uniform(43, 200000, 0.5, 2.0)
+    assert u.min() >= 0.5 and u.max() <= 2.0 and abs(u.mean() - 1.25) < 0.01
+    t = oracle.sm_student4(44, 200000).astype(np.float64)
+    # Student-t(4): median |x| = 0.7407
+    assert abs(np.median(np.abs(t)) - 0.7407) < 0.01
+
+
+def test_rel_err_metric(oracle):
+    a = np.array([1.0, 2.0, 3.5])
+    b = np.array([1.0, 2.0, 4.0])
+    assert oracle.rel_err(a, b) == pytest.approx(0.5 / 4.0)

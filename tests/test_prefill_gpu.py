@@ -1,0 +1,233 @@
+"""Prefill attention parity on the GPU, through the C ABI.
+
+Mirrors the reference's prefill gates (tests/test_prefill.cu:244-364, 849-866):
+the fp16 kernel against float64 causal attention at (m, P) = (64, 0),
+(100, 150), (37, 1000) with its 4e-3 absolute bound (and the north-star 2e-3
+relative bound); the int8 kernel on the lossless grid (within 1.01x of the fp16
+kernel's error), with every tile exact and smoothing on (the q.c shift must
+cancel), with mixed tiles and smoothing (2e-1), and -- stricter than the
+reference, which only reports random-data int8 error -- against the float64
+restatement of the same int8 algorithm (2e-3 relative) on every case.  The int8
+quantisers, the K mean and the int32 Q.K^T sums are checked bit-exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import abs_err, dev, dev_h, host, host_h, note
+
+pytestmark = pytest.mark.gpu
+
+SEED = 12345
+
+
+def _inputs(oracle, m, P, koff=0.0, with_off=False):
+    K, V, Q = oracle.mt_prefill_case(SEED, m, P, koff, with_off)
+    return K, V, Q
+
+
+class _Dev:
+    """Device copies of one case plus the int8 operands computed ON THE GPU."""
+
+    def __init__(self, lk, K, V, Q, m, P, smooth):
+        S = P + m
+        self.m, self.P, self.S = m, P, S
+        self.kstride = lk.kstride_for(S)
+        self.kc, self.vc, self.qh = dev_h(K), dev_h(V), dev_h(Q)
+        self.cm = torch.zeros(8, 64, device="cuda")
+        if smooth:
+            lk.pf_kmean(self.kc, S, self.cm)
+        cm = self.cm if smooth else None
+        self.q8 = torch.zeros(m, 2048, dtype=torch.int8, device="cuda")
+        self.qsc = torch.zeros(m, 32, device="cuda")
+        self.qcs = torch.zeros(m, 32, device="cuda")
+        self.k8 = torch.zeros(S * 512, dtype=torch.int8, device="cuda")
+        self.ksc = torch.zeros(8 * self.kstride + 4, device="cuda")
+        lk.pf_q8(self.qh, m, cm, self.q8, self.qsc, self.qcs)
+        lk.pf_k8(self.kc, 0, S, cm, self.kstride, self.k8, self.ksc)
+        torch.cuda.synchronize()
+
+    def attn8(self, lk, near, sink):
+        o = torch.full((self.m, 2048), float("nan"), device="cuda")
+        lk.pf_attn8(self.q8, self.qsc, self.qcs, self.qh, self.m, self.P, self.k8, self.ksc,
+                    self.kstride, self.kc, self.vc, near, sink, o)
+        torch.cuda.synchronize()
+        return host(o)
+
+    def attn16(self, lk):
+        o = torch.full((self.m, 2048), float("nan"), device="cuda")
+        lk.pf_attn(self.qh, self.m, self.P, self.kc, self.vc, o)
+        torch.cuda.synchronize()
+        return host(o)
+
+
+# ---- bit-exact pieces ------------------------------------------------------------------
+@pytest.mark.parametrize("smooth", [False, True])
+def test_quantisers_bit_exact(lk, oracle, smooth):
+    m, P = 100, 150
+    K, V, Q = _inputs(oracle, m, P, 3.0, True)
+    note(f"pf quantisers smooth={smooth}")
+    d = _Dev(lk, K, V, Q, m, P, smooth)
+    cm = oracle.pf_kmean(K, P + m) if smooth else None
+    if smooth:
+        assert np.array_equal(host(d.cm).view(np.uint32), cm.view(np.uint32))   # same order, same bits
+    q8, qsc, qcs = oracle.pf_q8(Q, m, cm)
+    assert np.array_equal(host(d.q8), q8)
+    assert np.array_equal(host(d.qsc).view(np.uint32), qsc.view(np.uint32))
+    assert np.array_equal(host(d.qcs).view(np.uint32), qcs.view(np.uint32))
+    k8, ksc = oracle.pf_k8(K, 0, P + m, d.kstride, cm)
+    assert np.array_equal(host(d.k8), k8)
+    assert np.array_equal(host(d.ksc)[:8 * d.kstride].view(np.uint32), ksc.view(np.uint32))
+
+
+def test_k8_incremental_range(lk, oracle):
+    # the engine re-quantises only [lo, pos0 + m) (reference engine.cu:1077-1084)
+    S, kstride = 300, 300
+    rng = np.random.default_rng(31)
+    K = (rng.standard_normal((S, 8, 64)) * 2).astype(np.float16).view(np.uint16)
+    kc = dev_h(K)
+    k8 = torch.full((S * 512,), 99, dtype=torch.int8, device="cuda")
+    ksc = torch.full((8 * kstride,), -1.0, device="cuda")
+    note("pf k8 incremental ranges")
+    lk.pf_k8(kc, 0, 37, None, kstride, k8, ksc)
+    lk.pf_k8(kc, 37, 37, None, kstride, k8, ksc)           # empty range: no-op
+    lk.pf_k8(kc, 37, 211, None, kstride, k8, ksc)
+    torch.cuda.synchronize()
+    rk8, rksc = oracle.pf_k8(K, 0, 211, kstride)
+    g8, gs = host(k8).reshape(S, 512), host(ksc).reshape(8, kstride)
+    assert np.array_equal(g8[:211], rk8.reshape(S, 512)[:211])
+    assert (g8[211:] == 99).all() and (gs[:, 211:] == -1.0).all()
+    assert np.array_equal(gs[:, :211].view(np.uint32), rksc.reshape(8, kstride)[:, :211].view(np.uint32))
+
+
+def test_qk_int32_bit_exact(lk, oracle):
+    rng = np.random.default_rng(32)
+    m, n = 48, 80
+    q8 = rng.integers(-127, 128, (m, 2048)).astype(np.int8)
+    k8 = rng.integers(-127, 128, (n, 8, 64)).astype(np.int8)
+    k8[0, :, :] = -127                                         # extreme sums
+    q8[0, :] = -127
+    s = torch.zeros(32, m, n, dtype=torch.int32, device="cuda")
+    note("pf int32 QK^T")
+    lk.pf_qk_i32(dev(q8), m, dev(k8), n, s)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(s), oracle.qk_i32(q8, m, k8, n))
+
+
+# ---- fp16 kernel ---------------------------------------------------------------------------
+@pytest.mark.parametrize("m,P", [(64, 0), (100, 150), (37, 1000), (1, 0), (1, 77), (130, 0), (200, 333)])
+def test_attn_fp16(lk, oracle, m, P):
+    K, V, Q = _inputs(oracle, m, P)
+    note(f"pf attn fp16 m={m} P={P}")
+    d = _Dev(lk, K, V, Q, m, P, False)
+    o = d.attn16(lk)
+    ref = oracle.pf_ref(Q, m, P, K, V)
+    e, rel = abs_err(o, ref), oracle.rel_err(o, ref)
+    note(f"  abs {e:.3e} rel {rel:.3e}")
+    assert e < 4e-3 and rel <= 2e-3
+
+
+def test_attn_first_row_is_v0(lk, oracle):
+    m, P = 40, 0
+    K, V, Q = _inputs(oracle, m, P)
+    note("pf attn: query 0 sees only key 0")
+    d = _Dev(lk, K, V, Q, m, P, False)
+    v0 = np.repeat(oracle.h2f(V[:512]).reshape(8, 64), 4, axis=0).reshape(-1)
+    assert np.array_equal(d.attn16(lk)[0], v0)
+    assert np.array_equal(d.attn8(lk, 0, 0)[0], v0)
+
+
+# ---- int8 kernel -----------------------------------------------------------------------------
+CASES8 = [
+    # (m, P, koff, smooth, near, gate) -- the reference's cases (test_prefill.cu:853-866)
+    (64, 0, -1.0, False, 0, "lossless"),
+    (100, 150, -1.0, False, 0, "lossless"),
+    (100, 150, 3.0, True, 1 << 20, "allexact"),
+    (37, 1000, 3.0, True, 1 << 20, "allexact"),
+    (37, 1000, 3.0, True, 256, "mixed"),
+    (100, 150, 0.0, False, 0, "info"),
+    (37, 1000, 3.0, False, 0, "info"),
+    (37, 1000, 3.0, True, 0, "info"),
+    # wider: several 64-row blocks, mixed exact/int8 inside a block, sink on
+    (300, 700, 0.0, False, 96, "info"),
+    (129, 2000, 1.0, False, 1024, "info"),
+]
+
+
+@pytest.mark.parametrize("m,P,koff,smooth,near,gate", CASES8,
+                         ids=[f"m{c[0]}_P{c[1]}_k{c[2]}_{'sm' if c[3] else 'ns'}_n{c[4]}" for c in CASES8])
+def test_attn8(lk, oracle, m, P, koff, smooth, near, gate):
+    K, V, Q = _inputs(oracle, m, P, koff, True)
+    sink = int(near > 0)
+    note(f"pf attn8 m={m} P={P} koff={koff} smooth={smooth} near={near}")
+    d = _Dev(lk, K, V, Q, m, P, smooth)
+    o8 = d.attn8(lk, near, sink)
+    o16 = d.attn16(lk)
+    ref = oracle.pf_ref(Q, m, P, K, V)
+    e8, e16 = abs_err(o8, ref), abs_err(o16, ref)
+    # the float64 restatement of the same int8 algorithm, on the GPU's int8 operands
+    ref8 = oracle.pf_ref8(host(d.q8), host(d.qsc), host(d.qcs), Q, m, P, host(d.k8), host(d.ksc),
+                          d.kstride, K, V, near, sink)
+    rel8 = oracle.rel_err(o8, ref8)
+    note(f"  int8 err {e8:.3e} (fp16 kernel {e16:.3e}); vs same-algorithm float64 rel {rel8:.3e}")
+    assert rel8 <= 2e-3
+    if gate in ("lossless", "allexact"):
+        assert e8 <= e16 * 1.01 + 1e-6
+    elif gate == "mixed":
+        assert e8 < 2e-1
+
+
+def test_attn8_deterministic(lk, oracle):
+    m, P = 200, 500
+    K, V, Q = _inputs(oracle, m, P, 1.0, True)
+    d = _Dev(lk, K, V, Q, m, P, True)
+    note("pf attn8 determinism")
+    a = d.attn8(lk, 128, 1)
+    for _ in range(3):
+        assert np.array_equal(d.attn8(lk, 128, 1).view(np.uint32), a.view(np.uint32))
+
+
+# ---- BASELINE prefill configurations (sampled rows against the float64 oracle) -----------------
+def _config_rows(m, long_ctx):
+    rows = {0, 63, 64, 1023, m - 1} if long_ctx else \
+        {0, 1, 31, 32, 63, 64, 65, 127, 128, 1000, 1023, 1024, 2047, 2048, m // 2 + 17, m - 2, m - 1}
+    return np.array(sorted(r for r in rows if r < m), np.int32)
+
+
+def _config_check(lk, oracle, qh, kc, vc, P, m, near, sink):
+    S = P + m
+    kstride = lk.kstride_for(S)
+    q8 = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
+    qsc = torch.empty(m, 32, device="cuda")
+    qcs = torch.empty(m, 32, device="cuda")
+    k8 = torch.empty(S * 512, dtype=torch.int8, device="cuda")
+    ksc = torch.empty(8 * kstride + 4, device="cuda")
+    qchunk = qh[P:P + m].contiguous()
+    lk.pf_q8(qchunk, m, None, q8, qsc, qcs)
+    lk.pf_k8(kc, 0, S, None, kstride, k8, ksc)
+    o = torch.empty(m, 2048, device="cuda")
+    lk.pf_attn8(q8, qsc, qcs, qchunk, m, P, k8, ksc, kstride, kc, vc, near, sink, o)
+    torch.cuda.synchronize()
+    rows = _config_rows(m, P > 0)
+    Kh = host_h(kc[:S]).reshape(-1)
+    Vh = host_h(vc[:S]).reshape(-1)
+    ref8 = oracle.pf_ref8(host(q8), host(qsc), host(qcs), host_h(qchunk), m, P, host(k8), host(ksc),
+                          kstride, Kh, Vh, near, sink, rows=rows)
+    rel = oracle.rel_err(host(o), ref8)
+    note(f"  rows {len(rows)}: rel vs same-algorithm float64 {rel:.3e}")
+    assert rel <= 2e-3
+    assert bool(torch.isfinite(o).all())
+
+
+def test_config_c4(lk, oracle):
+    import lk_configs
+    note("prefill config C4 (m=4096, P=0, near 1024, sink)")
+    qh, kc, vc, S = lk_configs.prefill_inputs("C4")
+    _config_check(lk, oracle, qh, kc, vc, 0, S, 1024, 1)
+
+
+def test_config_c5_last_chunk(lk, oracle):
+    import lk_configs
+    note("prefill config C5, last 4096 chunk at P=126976 (heavy-tailed Q/K)")
+    qh, kc, vc, S = lk_configs.prefill_inputs("C5")
+    _config_check(lk, oracle, qh, kc, vc, S - 4096, 4096, 1024, 1)
