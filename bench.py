@@ -1,0 +1,290 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention hot path on one MI355X.
+
+Headline (the `value`): decode attention HBM throughput at 32k context, the
+BASELINE's configs[1] -- 10 attention layers, each with its OWN 67 MB fp16 KV
+cache (670 MB in all, so the 256 MB MALL cannot serve the stream), captured as
+10 x (split, combine) in one hipGraph, the way the engine replays its decode
+step.  A step is one replay; bytes per layer are the reference's own count,
+seq x 2048 (K and V read once; bench_attn.cu:257-264).
+
+Also measured and reported under "results": C3 (131k x 10 layers, 2.7 GB),
+C4 (one 4096-token prefill chunk, int8 scores, near 1024, sink) and C5 (a
+131072-token prompt in 32 chunks of 4096), the per-kernel durations from HIP
+events recorded on the launch stream around every launch, and the CPU oracle
+(float64, single thread) as the reported CPU baseline.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-prefill] [--cpu-seconds S]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "lfm2-ampere_amd"))
+
+HBM_PEAK_GBS = 8000.0                 # MI355X HBM3E
+PEAK_INT8_TOPS = 5000.0               # dense int8 MFMA
+PEAK_FP16_TFLOPS = 2500.0             # dense fp16 MFMA
+REF_3090TI_GBS_32K = 669.3            # reference, RTX 3090 Ti, docs/ARCHITECTURE.md:2401
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_events(fn, stream, n):
+    """Average ms per call of fn() over n back-to-back calls on `stream`,
+    bracketed by one pair of HIP events (launch overhead amortised, so the
+    figure tracks the kernel's own duration as rocprof reports it)."""
+    import torch
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    stream.synchronize()
+    a.record(stream)
+    for _ in range(n):
+        fn()
+    b.record(stream)
+    stream.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters):
+    import torch
+    qs, kcs, vcs, seq = lkc.decode_inputs(cfg, layers=10)
+    layers = len(qs)
+    d_pos = torch.tensor([seq - 1], dtype=torch.int32, device="cuda")
+    part = torch.empty(lk.part_bytes() // 4, device="cuda")
+    outs = [torch.empty(32, 64, device="cuda") for _ in range(layers)]
+    graph = lk.DecodeGraph(qs, kcs, vcs, d_pos, part, outs)
+    st = graph.stream
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.launch()
+    st.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(steps):
+        graph.launch()
+    e1.record(st)
+    st.synchronize()
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / steps
+    bytes_layer = seq * 2048.0
+    us_layer = ms_step * 1e3 / layers
+    gbs = bytes_layer * layers / (ms_step * 1e-3) / 1e9
+    # per-kernel: the split kernel alone, rotating over the 10 layers' caches
+    i = [0]
+
+    def one_split():
+        j = i[0] % layers
+        i[0] += 1
+        lk.attn_split(qs[j], kcs[j], vcs[j], d_pos, part, stream=st)
+
+    one_split()
+    split_ms = timed_events(one_split, st, kernel_iters)
+    comb_ms = timed_events(lambda: lk.attn_combine(part, d_pos, outs[0], None, stream=st), st, kernel_iters)
+    graph.close()
+    res = {
+        "seq": seq, "layers": layers, "ms_per_step": ms_step, "us_per_layer": us_layer,
+        "GBps": gbs, "split_us": split_ms * 1e3, "combine_us": comb_ms * 1e3,
+        "split_GBps": bytes_layer / (split_ms * 1e-3) / 1e9, "bytes_per_layer": bytes_layer,
+        "graph_nodes": 2 * layers,
+    }
+    del qs, kcs, vcs
+    torch.cuda.empty_cache()
+    return res
+
+
+def pf_ops(m, P):
+    """Algorithmic ops of one causal chunk: per (query, key) pair 64 int8 MAC for
+    Q.K and 64 fp16 MAC for P.V, 2 ops per MAC (test_prefill.cu:652)."""
+    pairs = 32.0 * m * (P + (m + 1) / 2.0)
+    return pairs * 64 * 2, pairs * 64 * 2, pairs
+
+
+def bench_prefill_c4(lk, lkc, iters):
+    import torch
+    qh, kc, vc, S = lkc.prefill_inputs("C4")
+    m, P = S, 0
+    ks = lk.kstride_for(S)
+    st = torch.cuda.Stream()
+    q8 = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
+    qsc = torch.empty(m, 32, device="cuda")
+    qcs = torch.empty(m, 32, device="cuda")
+    k8 = torch.empty(S * 512, dtype=torch.int8, device="cuda")
+    ksc = torch.empty(8 * ks + 4, device="cuda")
+    o = torch.empty(m, 2048, device="cuda")
+    torch.cuda.synchronize()
+    q_ms = timed_events(lambda: lk.pf_q8(qh, m, None, q8, qsc, qcs, stream=st), st, iters)
+    k_ms = timed_events(lambda: lk.pf_k8(kc, 0, S, None, ks, k8, ksc, stream=st), st, iters)
+    f8 = lambda: lk.pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
+    f8()
+    a8_ms = timed_events(f8, st, iters)
+    f16 = lambda: lk.pf_attn(qh, m, P, kc, vc, o, stream=st)
+    f16()
+    a16_ms = timed_events(f16, st, iters)
+    oi, of, pairs = pf_ops(m, P)
+    peak_ms = (oi / (PEAK_INT8_TOPS * 1e12) + of / (PEAK_FP16_TFLOPS * 1e12)) * 1e3
+    return {
+        "m": m, "P": P, "near": 1024, "sink": 1, "pairs": pairs,
+        "attn8_us": a8_ms * 1e3, "attn8_TOPS": (oi + of) / (a8_ms * 1e-3) / 1e12,
+        "attn8_frac_of_mixed_peak": peak_ms / a8_ms,
+        "attn_fp16_us": a16_ms * 1e3, "attn_fp16_TOPS": (oi + of) / (a16_ms * 1e-3) / 1e12,
+        "q8_us": q_ms * 1e3, "k8_us": k_ms * 1e3,
+    }
+
+
+def bench_prefill_c5(lk, lkc, reps):
+    import torch
+    qh, kc, vc, S = lkc.prefill_inputs("C5")
+    m = 4096
+    ks = lk.kstride_for(S)
+    st = torch.cuda.Stream()
+    q8 = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
+    qsc = torch.empty(m, 32, device="cuda")
+    qcs = torch.empty(m, 32, device="cuda")
+    k8 = torch.empty(S * 512, dtype=torch.int8, device="cuda")
+    ksc = torch.empty(8 * ks + 4, device="cuda")
+    o = torch.empty(m, 2048, device="cuda")
+    qchunks = [qh[p:p + m].contiguous() for p in range(0, S, m)]
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(reps):
+        ev = []
+        for c, P in enumerate(range(0, S, m)):
+            a, b, c2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            a.record(st)
+            lk.pf_k8(kc, P, P + m, None, ks, k8, ksc, stream=st)
+            lk.pf_q8(qchunks[c], m, None, q8, qsc, qcs, stream=st)
+            b.record(st)
+            lk.pf_attn8(q8, qsc, qcs, qchunks[c], m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
+            c2.record(st)
+            ev.append((a, b, c2))
+        st.synchronize()
+        quant = sum(a.elapsed_time(b) for a, b, _ in ev)
+        attn = sum(b.elapsed_time(c2) for _, b, c2 in ev)
+        if best is None or attn < best[1]:
+            best = (quant, attn)
+    oi = of = 0.0
+    for P in range(0, S, m):
+        a, b, _ = pf_ops(m, P)
+        oi += a
+        of += b
+    quant_ms, attn_ms = best
+    peak_ms = (oi / (PEAK_INT8_TOPS * 1e12) + of / (PEAK_FP16_TFLOPS * 1e12)) * 1e3
+    del qh, kc, vc, qchunks, k8
+    torch.cuda.empty_cache()
+    return {
+        "chunks": S // m, "chunk": m, "attn_ms": attn_ms, "quant_ms": quant_ms,
+        "attn8_TOPS": (oi + of) / (attn_ms * 1e-3) / 1e12,
+        "attn8_frac_of_mixed_peak": peak_ms / attn_ms,
+    }
+
+
+def cpu_baseline(seconds):
+    """The oracle's float64 decode attention (the reference's CPU path,
+    tests/test_attn.cu:46-74), single-threaded, on C2 (ctx 32768) and C1."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import lk_oracle as orc
+    import lk_configs as lkc
+    res = {}
+    for cfg, budget in (("C2", seconds), ("C1", max(2.0, seconds / 5))):
+        qs, kcs, vcs, seq = lkc.decode_inputs(cfg, layers=1)
+        q = qs[0].cpu().numpy()
+        kh = kcs[0].view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+        vh = vcs[0].view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+        n, t0 = 0, time.perf_counter()
+        while True:
+            orc.decode_ref(q, kh, vh, seq)
+            n += 1
+            if time.perf_counter() - t0 >= budget:
+                break
+        dt = (time.perf_counter() - t0) / n
+        res[cfg] = {"us_per_layer": dt * 1e6, "GBps": seq * 2048.0 / dt / 1e9, "reps": n}
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--kernel-iters", type=int, default=100)
+    ap.add_argument("--skip-prefill", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this attention path is built and measured on a single "
+              "MI355X (no multi-GPU path); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import lk_attn as lk
+    import lk_configs as lkc
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    lk.load()
+    cfgp = lk.config()
+
+    log("decode C2 (32k x 10 layers, one hipGraph)")
+    c2 = bench_decode(lk, lkc, "C2", args.steps, args.warmup, args.kernel_iters)
+    log(json.dumps(c2))
+    log("decode C3 (131k x 10 layers, one hipGraph)")
+    c3 = bench_decode(lk, lkc, "C3", max(20, args.steps // 4), max(3, args.warmup // 4), args.kernel_iters // 2)
+    log(json.dumps(c3))
+    results = {"C2_decode_32k": c2, "C3_decode_131k": c3}
+    if not args.skip_prefill:
+        log("prefill C4 (4096 chunk, P=0)")
+        results["C4_prefill_4k"] = bench_prefill_c4(lk, lkc, 20)
+        log(json.dumps(results["C4_prefill_4k"]))
+        log("prefill C5 (131072 prompt, 32 chunks)")
+        results["C5_prefill_131k"] = bench_prefill_c5(lk, lkc, 2)
+        log(json.dumps(results["C5_prefill_131k"]))
+
+    cpu = None
+    if not args.skip_cpu:
+        log("cpu baseline (float64 oracle, 1 thread)")
+        cb = cpu_baseline(args.cpu_seconds)
+        results["cpu_float64"] = cb
+        cpu = {"value": cb["C2"]["GBps"], "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"full C2 layer (32q/8kv/64, ctx 32768) float64 decode attention, "
+                         f"{cb['C2']['reps']} repetitions, {cb['C2']['us_per_layer']:.0f} us/layer; "
+                         f"host nproc {os.cpu_count()}"}
+
+    ach = c2["split_GBps"]
+    line = {
+        "metric": "decode attn us/layer + HBM GB/s @32k/131k; prefill attn TOPS @4k/131k",
+        "value": round(c2["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(c2["GBps"] / REF_3090TI_GBS_32K, 3),
+        "dtype": "fp16",
+        "data": "synthetic (seeded device generator, BASELINE configs C2-C5)",
+        "config": {
+            "workload": "C2: decode attention, ctx 32768, 32q/8kv/64, 10 layers with distinct "
+                        "fp16 KV caches replayed as one hipGraph of 10 x (split, combine)",
+            "seq": c2["seq"], "layers": c2["layers"], "us_per_layer": round(c2["us_per_layer"], 3),
+            "split_cap": cfgp["split_cap"], "target_n": cfgp["target_n"], "split_min": cfgp["split_min"],
+            "baseline": "reference on RTX 3090 Ti: 669.3 GB/s, 100.27 us/layer @32768",
+        },
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "lk_k_attn_split (C2, seq x 2048 B per launch)"},
+        "cpu_baseline": cpu,
+        "results": results,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -34,7 +34,7 @@ extern "C" {
 #define LK_N_HEADS      32
 #define LK_N_KV_HEADS   8
 #define LK_HEAD_DIM     64
-#define LK_ATTN_PARTW   (2 + LK_HEAD_DIM)   /* partial record: m, l, acc[64] */
+#define LK_ATTN_PARTW   (4 + LK_HEAD_DIM)   /* partial record: m, l, 2 pad, acc[64] */
 
 /* Q8_1 activation block (reference quant.cuh:27-31): fp16 d = amax/127 and
  * fp16 raw sum of the 32 values, then the 32 int8 quants.  36 bytes. */
@@ -51,7 +51,7 @@ typedef struct lk_block_q8_1 {
  * (reference kernels.cuh:630-635, retuned for 256 CUs). */
 int lk_attn_config(int * split_cap, int * target_n, int * split_min);
 
-/* Bytes the caller must allocate for `part` (fp32 [32][split_cap][66]).
+/* Bytes the caller must allocate for `part` (fp32 [32][split_cap][68]).
  * Replaces the engine's own sizing at reference engine.cu:408-409. */
 size_t lk_attn_part_bytes(void);
 
@@ -63,13 +63,14 @@ const char * lk_last_error(void);
  * kc  : fp16 [max_seq][8][64] K cache of this layer
  * vc  : fp16 [max_seq][8][64] V cache of this layer
  * d_pos: int32, device; the kernels attend to positions [0, *d_pos]
- * part: fp32 scratch of lk_attn_part_bytes() bytes
+ * part: fp32 scratch of lk_attn_part_bytes() bytes (slice partials)
  * out : fp32 [32][64] or NULL
  * yq8 : lk_block_q8_1 [64] (two blocks per head) or NULL
  */
 
 /* Replaces k_attn_split (reference kernels.cuh:647-649, kernels.cu:1303-1556).
- * Grid (8 kv heads x split_cap), blocks past the live slice count exit. */
+ * Grid (split_cap) of 8-wave workgroups, each over all 8 kv heads of one
+ * contiguous slice of positions; workgroups past the live slice count exit. */
 int lk_attn_split(const float * q, const void * kc, const void * vc,
                   const int * d_pos, float * part, void * stream);
 

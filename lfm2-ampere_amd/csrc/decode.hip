@@ -35,31 +35,116 @@ __device__ __forceinline__ void lk_split_h(float x, _Float16 & hi, _Float16 & lo
     lo = (_Float16) (x - (float) hi);
 }
 
-template <int U>
-__global__ void __launch_bounds__(256)
+// ---- decode split kernel ------------------------------------------------------
+// The workgroup of slice sp covers ALL 8 kv heads of positions [t0, t1): cache
+// rows (one position = 8 heads x 64 dims = 1 KB of K, same of V) are fetched
+// whole, 64 lanes x 16 contiguous bytes per instruction, straight into LDS
+// (global_load_lds_dwordx4, no staging registers), into a ring of LK_DEC_NBUF
+// tiles of LK_DEC_TILE positions; LK_DEC_NBUF-1 tiles are in flight while one
+// is consumed.  Whole-row streaming is what lets HBM run near its peak: a
+// per-head walk touches 128 of every 1024 bytes and measured ~40% slower.
+// Wave w then serves kv head w (its 4 query heads) from the LDS tile.
+// LDS rows are padded by 16 bytes so 16 lanes reading 16 bytes from 16
+// consecutive rows hit 16 different bank groups.
+#define LK_DEC_ROWB    (LK_KV_ROW * 2 + 16)                   // bytes per LDS row
+#define LK_DEC_TILEB   (2 * LK_DEC_TILE * LK_DEC_ROWB)         // K rows + V rows
+#define LK_DEC_THREADS 512                                     // 8 waves = 8 kv heads
+// Measurement-only ablation (any non-zero value gives WRONG output): 1 = skip
+// the P.V accumulate, 2 = skip Q.K^T and the softmax, 3 = skip both (the
+// kernel then only streams K and V through LDS).
+#ifndef LK_DEC_ABLATE
+#define LK_DEC_ABLATE 0
+#endif
+
+// Byte address of an LDS object (the value M0 takes for an LDS DMA).
+__device__ __forceinline__ uint32_t lk_lds_addr(const void * p) {
+    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) p;
+}
+// One LDS DMA: each lane's 16 bytes at `src` land at LDS byte lds + 16*lane,
+// non-temporal (the KV stream is read once).  Issued as inline asm so the
+// compiler does not serialise later LDS reads on it; completion is tracked by
+// hand with vmcnt (in-order) plus a barrier.  M0 is written here; nothing else
+// in the decode kernels uses M0, so clobbering it is safe.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lk_dma16(const void * src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :: "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void lk_wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+__global__ void __launch_bounds__(LK_DEC_THREADS)
 lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
                 const _Float16 * __restrict__ vc, const int * __restrict__ d_pos,
                 float * __restrict__ part) {
+    constexpr int RPW = 2 * LK_DEC_TILE / 8;                   // rows fetched per wave per tile
+    constexpr int NG  = LK_DEC_TILE / 16;                      // 16-token groups per tile
+    constexpr int D   = LK_DEC_NBUF - 1;                       // tiles in flight
+    static_assert(LK_DEC_TILE % 16 == 0 && LK_DEC_NBUF >= 2, "decode tile shape");
+    __shared__ __attribute__((aligned(16))) unsigned char s_tile[LK_DEC_NBUF][LK_DEC_TILEB];
+
     const int seq = *d_pos + 1;
     int ns, chunk;
     lk_attn_slices(seq, ns, chunk);
-    const int kvh = blockIdx.x, sp = blockIdx.y;
+    const int sp = blockIdx.x;
     const int t0 = sp * chunk;
     const int t1 = (t0 + chunk < seq) ? (t0 + chunk) : seq;
     // Block-uniform early out before any barrier: dead slices write nothing
     // (the combine derives the same boundary and never reads them).
     if (t0 >= t1) return;
     const int n = t1 - t0;
+    const int ntile = (n + LK_DEC_TILE - 1) / LK_DEC_TILE;
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave = kv head
     const int col = lane & 15, g = lane >> 4;
 
-    // A operand: row i = col carries query head kvh*4 + (i & 3); k-slots 8g..8g+7
+    // ---- fetch: wave w brings rows w, w+8, ... of each tile (K rows first) ----
+    const char * kg = (const char *) (kc + (size_t) t0 * LK_KV_ROW) + 16 * lane;
+    const char * vg = (const char *) (vc + (size_t) t0 * LK_KV_ROW) + 16 * lane;
+    const uint32_t lds0 = lk_lds_addr(&s_tile[0][0]);
+    auto fetch = [&](int it) {
+        const uint32_t base = lds0 + (uint32_t) ((it % LK_DEC_NBUF) * LK_DEC_TILEB);
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            const int row = w + 8 * i;                         // 0 .. 2*TILE-1
+            const bool isv = row >= LK_DEC_TILE;
+            const int tt = it * LK_DEC_TILE + (isv ? row - LK_DEC_TILE : row);
+            const size_t o = (size_t) (tt < n ? tt : 0) * (LK_KV_ROW * 2);   // clamp: t0 is in range
+            lk_dma16((isv ? vg : kg) + o, base + (uint32_t) (row * LK_DEC_ROWB));
+        }
+    };
+    // Wait until tile `it` is resident for the whole workgroup.  When tile it
+    // is awaited, this wave has issued tiles up to min(it + D - 1, ntile - 1)
+    // (tile it + D is fetched only after tile it is consumed); its own fetches
+    // complete in order, so the rows of those later tiles may stay pending.
+    // The barrier then covers the other waves' rows.
+    auto wait_tile = [&](int it) {
+        const int later = (ntile - 1 - it < D - 1) ? ntile - 1 - it : D - 1;
+        if (later >= 2)      lk_wait_vm<2 * RPW>();
+        else if (later == 1) lk_wait_vm<RPW>();
+        else                 lk_wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+    };
+    static_assert(D - 1 <= 2, "wait_tile handles at most two later tiles in flight");
+
+    // issue the first D tiles before anything else, so HBM starts streaming at once
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+        if (i < ntile) fetch(i);
+
+    // A operand: row i = col carries query head 4w + (i & 3); k-slots 8g..8g+7
     // of MFMA 0 are dims 16g..16g+7, of MFMA 1 dims 16g+8..16g+15 -- the same
-    // dims this lane loads of its token, so A and B agree slot by slot.
+    // dims this lane reads of its token, so A and B agree slot by slot.
     lk_h8 qa0h, qa0l, qa1h, qa1l;
     {
-        const float * qp = q + (kvh * LK_G + (col & 3)) * LK_HEAD_DIM + 16 * g;
+        const float * qp = q + (w * LK_G + (col & 3)) * LK_HEAD_DIM + 16 * g;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             _Float16 h, l;
@@ -77,107 +162,100 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
         for (int k = 0; k < 16; ++k) acc[r][k] = 0.0f;
     }
 
-    const size_t lane_off = (size_t) kvh * LK_HEAD_DIM + 16 * g;
-    const _Float16 * kb = kc + (size_t) t0 * LK_KV_ROW + lane_off;
-    const _Float16 * vb = vc + (size_t) t0 * LK_KV_ROW + lane_off;
-
-    for (int j0 = 16 * w; j0 < n; j0 += 64 * U) {
-        lk_h8 k0[U], k1[U], v0[U], v1[U];
-        bool ok[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = j0 + 64 * u + col;
-            ok[u] = j < n;
-            // dead lanes read token t0 (always in range) and are masked below
-            const size_t o = (size_t) (ok[u] ? j : 0) * LK_KV_ROW;
-            k0[u] = *(const lk_h8 *) (kb + o);
-            k1[u] = *(const lk_h8 *) (kb + o + 8);
-            v0[u] = *(const lk_h8 *) (vb + o);
-            v1[u] = *(const lk_h8 *) (vb + o + 8);
-        }
-        float s[U][4];
+    // ---- consume one tile: wave w = kv head w, NG groups of 16 tokens --------
+    auto consume = [&](const unsigned char * buf, int it) {
+#if LK_DEC_ABLATE == 3
+        if (buf[lane] == 0x7f && it < 0) lrun[0] += 1.0f;
+        return;
+#endif
+        float s[NG][4];
         float mloc[4] = { -INFINITY, -INFINITY, -INFINITY, -INFINITY };
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int gi = 0; gi < NG; ++gi) {
+            const unsigned char * kr = buf + (16 * gi + col) * LK_DEC_ROWB + w * 128 + 32 * g;
             lk_f4 c = { 0.0f, 0.0f, 0.0f, 0.0f };
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa0h, k0[u], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa0l, k0[u], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa1h, k1[u], c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa1l, k1[u], c, 0, 0, 0);
+#if LK_DEC_ABLATE == 2
+            s[gi][0] = s[gi][1] = s[gi][2] = s[gi][3] = (float) col;
+            continue;
+#endif
+            const lk_h8 k0 = *(const lk_h8 *) kr;
+            const lk_h8 k1 = *(const lk_h8 *) (kr + 16);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa0h, k0, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa0l, k0, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa1h, k1, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa1l, k1, c, 0, 0, 0);
+            const bool ok = it * LK_DEC_TILE + 16 * gi + col < n;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                s[u][r] = ok[u] ? c[r] * SC : -INFINITY;
-                mloc[r] = fmaxf(mloc[r], s[u][r]);
+                s[gi][r] = ok ? c[r] * SC : -INFINITY;
+                mloc[r] = fmaxf(mloc[r], s[gi][r]);
             }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+            const float mnew = fmaxf(mrun[r], lk_row_max16(mloc[r]));
+            // every lane holds the same mnew (rows replicate the same tokens),
+            // so this branch is wave-uniform; most tiles do not raise the max
+            if (mnew > mrun[r]) {
+                const float alpha = lk_exp2(mrun[r] - mnew);
+                mrun[r] = mnew;
+                lrun[r] *= alpha;
 #pragma unroll
-            for (int o = 1; o < 16; o <<= 1) mloc[r] = fmaxf(mloc[r], __shfl_xor(mloc[r], o, 64));
-            const float mnew = fmaxf(mrun[r], mloc[r]);
-            const float alpha = lk_exp2(mrun[r] - mnew);
-            mrun[r] = mnew;
-            lrun[r] *= alpha;
-#pragma unroll
-            for (int k = 0; k < 16; ++k) acc[r][k] *= alpha;
+                for (int k = 0; k < 16; ++k) acc[r][k] *= alpha;
+            }
         }
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int gi = 0; gi < NG; ++gi) {
+            const unsigned char * vr = buf + (LK_DEC_TILE + 16 * gi + col) * LK_DEC_ROWB + w * 128 + 32 * g;
+#if LK_DEC_ABLATE == 1
+            lrun[0] += s[gi][0];
+            continue;
+#endif
+            const lk_h8 v0 = *(const lk_h8 *) vr;
+            const lk_h8 v1 = *(const lk_h8 *) (vr + 16);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = lk_exp2(s[u][r] - mrun[r]);
+                const float p = lk_exp2(s[gi][r] - mrun[r]);
                 lrun[r] += p;
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
-                    acc[r][k]     += p * (float) v0[u][k];
-                    acc[r][8 + k] += p * (float) v1[u][k];
+                    acc[r][k]     += p * (float) v0[k];
+                    acc[r][8 + k] += p * (float) v1[k];
                 }
             }
         }
+    };
+
+    for (int it = 0; it < ntile; ++it) {
+        wait_tile(it);
+        consume(s_tile[it % LK_DEC_NBUF], it);
+        // every wave is done reading buffer it % NBUF before it is refilled
+        __builtin_amdgcn_s_barrier();
+        if (it + D < ntile) fetch(it + D);
     }
 
-    // Sum the 16 token lanes of each row group (fixed butterfly): afterwards
+    // Sum the 16 token lanes of each row (fixed DPP butterfly): afterwards
     // every lane of row group g holds l and acc for dims 16g..16g+15.
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+        lrun[r] = lk_row_sum16(lrun[r]);
 #pragma unroll
-        for (int o = 1; o < 16; o <<= 1) {
-            lrun[r] += __shfl_xor(lrun[r], o, 64);
+        for (int k = 0; k < 16; ++k) acc[r][k] = lk_row_sum16(acc[r][k]);
+    }
+    // Partial record of query head 4w + r: lane col == r of row group g writes
+    // dims 16g..16g+15 (as four 16-byte stores); lane 0 of the row writes m, l.
+    if (col < 4) {
+        const int r = col;
+        float * P = part + ((size_t) (w * LK_G + r) * LK_ATTN_SPLIT + sp) * LK_ATTN_PARTW;
+        float a[16];
 #pragma unroll
-            for (int k = 0; k < 16; ++k) acc[r][k] += __shfl_xor(acc[r][k], o, 64);
+        for (int k = 0; k < 16; ++k) a[k] = (r == 0) ? acc[0][k] : (r == 1) ? acc[1][k] : (r == 2) ? acc[2][k] : acc[3][k];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) P[4 + 16 * g + k] = a[k];
+        if (g == 0) {
+            P[0] = (r == 0) ? mrun[0] : (r == 1) ? mrun[1] : (r == 2) ? mrun[2] : mrun[3];
+            P[1] = (r == 0) ? lrun[0] : (r == 1) ? lrun[1] : (r == 2) ? lrun[2] : lrun[3];
         }
-    }
-
-    __shared__ float s_m[4][4], s_l[4][4];
-    __shared__ float s_acc[4][4][LK_HEAD_DIM];
-    if (col == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int k = 0; k < 16; ++k) s_acc[w][r][16 * g + k] = acc[r][k];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) { s_m[w][r] = mrun[r]; s_l[w][r] = lrun[r]; }
-    }
-    __syncthreads();
-    {
-        // thread -> (head r, dim d); waves merged in the fixed order 0,1,2,3.
-        // A wave that owned no tokens holds m = -1e30, l = 0: weight 0.
-        const int r = threadIdx.x >> 6, d = threadIdx.x & 63;
-        float M = s_m[0][r];
-#pragma unroll
-        for (int ww = 1; ww < 4; ++ww) M = fmaxf(M, s_m[ww][r]);
-        float L = 0.0f, A = 0.0f;
-#pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
-            const float e = lk_exp2(s_m[ww][r] - M);
-            L += s_l[ww][r] * e;
-            A += s_acc[ww][r][d] * e;
-        }
-        float * P = part + ((size_t) (kvh * LK_G + r) * LK_ATTN_SPLIT + sp) * LK_ATTN_PARTW;
-        if (d == 0) { P[0] = M; P[1] = L; }
-        P[2 + d] = A;
     }
 }
 
@@ -204,52 +282,96 @@ __device__ __forceinline__ void lk_quant_q8_1_wave(float x, lk_block_q8_1 * __re
     }
 }
 
-// One workgroup per query head, 256 threads.  Slices s with s*chunk >= seq hold
-// no tokens and are skipped (reference kernels.cu:1573-1584).  Slice weights
-// are 2^(m_s - M); thread group j (64 lanes, one per dim) folds the j-th
-// contiguous quarter of the slices serially, and the four quarter sums are
-// added in the order 0,1,2,3: a fixed order, so output is bit-reproducible.
+// The same quantiser for one 32-value block held by lanes 0..31 of a wave
+// (lanes 32..63 hold a copy and write nothing).
+__device__ __forceinline__ void lk_quant_q8_1_half(float x, lk_block_q8_1 * __restrict__ b) {
+    const int lane = threadIdx.x & 63;
+    float am = fabsf(x), sum = x;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+        am = fmaxf(am, __shfl_xor(am, o, 32));
+        sum += __shfl_xor(sum, o, 32);
+    }
+    const float d = am / 127.0f;
+    const int8_t qv = (am == 0.0f) ? (int8_t) 0 : (int8_t) roundf(x / d);
+    if (lane < 32) b->qs[lane] = qv;
+    if (lane == 0) {
+        const _Float16 dh = (_Float16) d, sh = (_Float16) sum;
+        b->d = __builtin_bit_cast(uint16_t, dh);
+        b->s = __builtin_bit_cast(uint16_t, sh);
+    }
+}
+
+// Combine: grid (32 query heads, 2 halves of the 64 dims), 256 threads, one
+// slice per thread.  Slices s with s*chunk >= seq hold no tokens and are
+// skipped (reference kernels.cu:1573-1584).  Each thread requests its slice's
+// (m, l) and 32 acc values at once (one memory round trip), the block max M is
+// exact, the slice weights are 2^(m_s - M), and the weighted values are summed
+// in a fixed order: 8 segments of 32 consecutive slices serially, then the 8
+// segment sums in index order.  Fixed order => bit-reproducible output.  Each
+// half is exactly one Q8_1 block of the next GEMV's input.
+static_assert(LK_ATTN_SPLIT <= 256 && LK_ATTN_SPLIT % 32 == 0, "combine assumes <= 256 slices");
+__device__ __forceinline__ float lk_wave_max(float v) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
 __global__ void __launch_bounds__(256)
 lk_k_attn_combine(const float * __restrict__ part, const int * __restrict__ d_pos,
                   float * __restrict__ out, lk_block_q8_1 * __restrict__ yq8) {
-    const int head = blockIdx.x;
+    const int head = blockIdx.x, half = blockIdx.y;
     const int seq = *d_pos + 1;
     int ns, chunk;
     lk_attn_slices(seq, ns, chunk);
     const int nv = (seq + chunk - 1) / chunk;        // non-empty slices, <= ns
-    const float * P = part + (size_t) head * LK_ATTN_SPLIT * LK_ATTN_PARTW;
+    const int s = threadIdx.x, lane = s & 63, wv = s >> 6;
+    const bool live = s < nv;
+    const float * R = part + ((size_t) head * LK_ATTN_SPLIT + (live ? s : 0)) * LK_ATTN_PARTW;
 
-    __shared__ float s_red[256];
-    float mx = -1e30f;
-    for (int s = threadIdx.x; s < nv; s += 256) mx = fmaxf(mx, P[(size_t) s * LK_ATTN_PARTW]);
-    s_red[threadIdx.x] = mx;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if ((int) threadIdx.x < o) s_red[threadIdx.x] = fmaxf(s_red[threadIdx.x], s_red[threadIdx.x + o]);
-        __syncthreads();
-    }
-    const float M = s_red[0];
+    lk_f4 a[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = *(const lk_f4 *) (R + 4 + 32 * half + 4 * i);
+    const lk_f4 ml = *(const lk_f4 *) R;             // m, l, pad, pad
+    const float m = live ? ml[0] : -1e30f;
 
-    const int d = threadIdx.x & 63, j = threadIdx.x >> 6;
-    const int q4 = (nv + 3) >> 2;
-    const int sb = j * q4, se = (sb + q4 < nv) ? sb + q4 : nv;
-    float L = 0.0f, A = 0.0f;
-    for (int s = sb; s < se; ++s) {
-        const float * ps = P + (size_t) s * LK_ATTN_PARTW;
-        const float e = lk_exp2(ps[0] - M);
-        L += ps[1] * e;
-        A += ps[2 + d] * e;
-    }
-    __shared__ float s_a[4][64], s_l[4];
-    s_a[j][d] = A;
-    if (d == 0) s_l[j] = L;
+    __shared__ float s_red[4];
+    __shared__ float s_v[256][33];                   // weighted values, col 32 = l*w
+    __shared__ float s_seg[8][33];
+    const float mx = lk_wave_max(m);
+    if (lane == 0) s_red[wv] = mx;
     __syncthreads();
-    if (j == 0) {
-        const float Af = ((s_a[0][d] + s_a[1][d]) + s_a[2][d]) + s_a[3][d];
-        const float Lf = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
-        const float o = Af * (1.0f / Lf);
-        if (out) out[head * LK_HEAD_DIM + d] = o;
-        if (yq8) lk_quant_q8_1_wave(o, yq8 + 2 * head);
+    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    const float wgt = live ? lk_exp2(m - M) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) s_v[s][4 * i + k] = a[i][k] * wgt;
+    s_v[s][32] = live ? ml[1] * wgt : 0.0f;
+    __syncthreads();
+    // 8 segments x 33 columns: thread (column c, segment j) sums 32 slices in order
+    {
+        const int c = s & 63, j = s >> 6;           // c < 33 used; j = 0..3 covers 2 segments each
+        if (c < 33) {
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int seg = 2 * j + jj;
+                float t = 0.0f;
+#pragma unroll 8
+                for (int i = 0; i < 32; ++i) t += s_v[32 * seg + i][c];
+                s_seg[seg][c] = t;
+            }
+        }
+    }
+    __syncthreads();
+    if (wv == 0) {
+        const int c = lane & 31;
+        float A = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { A += s_seg[j][c]; L += s_seg[j][32]; }
+        const float o = A * (1.0f / L);
+        if (out && lane < 32) out[head * LK_HEAD_DIM + 32 * half + c] = o;
+        if (yq8) lk_quant_q8_1_half(o, yq8 + 2 * head + half);
     }
 }
 
@@ -313,14 +435,13 @@ lk_k_attention_decode(const float * __restrict__ q, const _Float16 * __restrict_
 // C ABI
 static int lk_split_launch(const float * q, const void * kc, const void * vc,
                            const int * d_pos, float * part, hipStream_t st) {
-    hipLaunchKernelGGL(lk_k_attn_split<LK_ATTN_UNROLL>, dim3(LK_N_KV_HEADS, LK_ATTN_SPLIT),
-                       dim3(256), 0, st, q, (const _Float16 *) kc, (const _Float16 *) vc,
-                       d_pos, part);
+    hipLaunchKernelGGL(lk_k_attn_split, dim3(LK_ATTN_SPLIT), dim3(LK_DEC_THREADS), 0, st,
+                       q, (const _Float16 *) kc, (const _Float16 *) vc, d_pos, part);
     return lk_launch_status("lk_attn_split");
 }
 static int lk_combine_launch(const float * part, const int * d_pos, float * out,
                              lk_block_q8_1 * yq8, hipStream_t st) {
-    hipLaunchKernelGGL(lk_k_attn_combine, dim3(LK_N_HEADS), dim3(256), 0, st, part, d_pos, out, yq8);
+    hipLaunchKernelGGL(lk_k_attn_combine, dim3(LK_N_HEADS, 2), dim3(256), 0, st, part, d_pos, out, yq8);
     return lk_launch_status("lk_attn_combine");
 }
 

@@ -25,9 +25,13 @@
 #ifndef LK_ATTN_SPLIT_MIN
 #define LK_ATTN_SPLIT_MIN  8
 #endif
-// 16-token groups a decode wave loads before it consumes any of them.
-#ifndef LK_ATTN_UNROLL
-#define LK_ATTN_UNROLL     4
+// Decode LDS ring: LK_DEC_NBUF tiles of LK_DEC_TILE cache positions (multiple
+// of 16); LK_DEC_NBUF - 1 of them are in flight while one is consumed.
+#ifndef LK_DEC_TILE
+#define LK_DEC_TILE        16
+#endif
+#ifndef LK_DEC_NBUF
+#define LK_DEC_NBUF        3
 #endif
 
 // ---- vector types ---------------------------------------------------------------
@@ -37,6 +41,39 @@ typedef float    lk_f4  __attribute__((ext_vector_type(4)));
 typedef int      lk_i4  __attribute__((ext_vector_type(4)));
 
 #define LK_LOG2E_F 1.4426950408889634f
+
+// ---- cross-lane reductions over one 16-lane row (DPP, no LDS traffic) ------
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror: a
+// fixed butterfly after which EVERY lane of the row holds the same total
+// (lane i and its partner add the same two operands, so the bits agree).
+#define LK_DPP_QP_XOR1   0xB1
+#define LK_DPP_QP_XOR2   0x4E
+#define LK_DPP_HMIRROR   0x141
+#define LK_DPP_MIRROR    0x140
+#ifdef __HIP_DEVICE_COMPILE__
+template <int CTRL>
+__device__ __forceinline__ float lk_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+#else
+template <int CTRL>
+__device__ __forceinline__ float lk_dpp(float v) { return v; }
+#endif
+__device__ __forceinline__ float lk_row_sum16(float v) {
+    v += lk_dpp<LK_DPP_QP_XOR1>(v);
+    v += lk_dpp<LK_DPP_QP_XOR2>(v);
+    v += lk_dpp<LK_DPP_HMIRROR>(v);
+    v += lk_dpp<LK_DPP_MIRROR>(v);
+    return v;
+}
+__device__ __forceinline__ float lk_row_max16(float v) {
+    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR1>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR2>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_HMIRROR>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_MIRROR>(v));
+    return v;
+}
 
 // 2^x on the transcendental unit (v_exp_f32); 2^-inf = 0.
 __device__ __forceinline__ float lk_exp2(float x) {

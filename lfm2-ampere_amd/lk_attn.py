@@ -18,7 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblk_attn.so")
 
 N_HEADS, N_KV_HEADS, HEAD_DIM = 32, 8, 64
-PARTW = 2 + HEAD_DIM
+PARTW = 4 + HEAD_DIM
 DECODE_MAX_SEQ = 8192
 Q8_1_BYTES = 36
 

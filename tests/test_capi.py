@@ -32,7 +32,7 @@ def test_config_and_part_size():
     import lk_attn
     c = lk_attn.config()
     assert c["split_min"] >= 1 and c["target_n"] >= 16 and c["split_cap"] >= c["split_min"]
-    assert lk_attn.part_bytes() == 32 * c["split_cap"] * 66 * 4
+    assert lk_attn.part_bytes() == 32 * c["split_cap"] * lk_attn.PARTW * 4
 
 
 def test_slice_rule_binding_matches_oracle(oracle):
