@@ -75,6 +75,27 @@ __device__ __forceinline__ float lk_row_max16(float v) {
     return v;
 }
 
+// Max over the four 16-lane rows holding the same column (lanes l, l^16,
+// l^32, l^48), with the gfx950 lane swaps (VALU, no LDS round trip):
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with the
+// lower 32 of its second, v_permlane16_swap the odd 16-lane rows of the first
+// with the even rows of the second.  Swapping a value with a copy of itself
+// leaves each lane holding itself and its partner; their max is symmetric, so
+// all four lanes end with identical bits.  Written as inline asm (with the
+// wait states the VALU -> permlane hazard needs) because the compiler folds
+// max(r0, r1) of the builtin's two results to r0, which is wrong.
+#ifdef __HIP_DEVICE_COMPILE__
+__device__ __forceinline__ float lk_xrow_max(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    float c = fmaxf(a, b), d = c;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
+    return fmaxf(c, d);
+}
+#else
+__device__ __forceinline__ float lk_xrow_max(float x) { return x; }
+#endif
+
 // 2^x on the transcendental unit (v_exp_f32); 2^-inf = 0.
 __device__ __forceinline__ float lk_exp2(float x) {
 #if defined(__HIP_DEVICE_COMPILE__)

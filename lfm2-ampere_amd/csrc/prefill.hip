@@ -105,22 +105,26 @@ lk_k_pf_kmean(const _Float16 * __restrict__ kc, int n, float * __restrict__ cm) 
 
 // ---------------------------------------------------------------------------
 // Flash attention.
-#define PF_BQ      64                     // query rows per workgroup
-#define PF_BK      64                     // keys per tile
-#define PF_QB      (PF_BQ / 16)           // 16-query blocks per wave
+#define PF_BQ      64                     // query rows per workgroup (16 per block)
+#define PF_BK      32                     // keys per tile (two 16-key blocks)
+#define PF_QB      (PF_BQ / 16)
 #define PF_K8_LD   80                     // LDS row pitch (bytes) of the int8 K tile
-#define PF_KH_LD   72                     // LDS row pitch (halves) of the fp16 K tile
-#define PF_VT_LD   68                     // LDS row pitch (halves) of the V^T tile
+#define PF_KH_LD   144                    // LDS row pitch (bytes) of the fp16 K tile
+#define PF_V_LD    144                    // LDS row pitch (bytes) of the fp16 V tile
+#define PF_Q_LD    144                    // LDS row pitch (bytes) of the fp16 Q block
 
 struct alignas(16) PfStage {
     int8_t   k8[PF_BK * PF_K8_LD];        // [key][64 B + pad]
-    _Float16 kh[PF_BK * PF_KH_LD];        // [key][64 + pad]
-    _Float16 vt[LK_HEAD_DIM * PF_VT_LD];  // [dim][64 keys + pad]
+    int8_t   kh[PF_BK * PF_KH_LD];        // [key][64 fp16 + pad]
+    int8_t   v[PF_BK * PF_V_LD];          // [key][64 fp16 + pad], row-major
     float    ks[PF_BK];                   // int8 K scales of the tile
 };
 
-__device__ __forceinline__ bool lk_pf_exact(int P, int qt32, int kt, int near, int sink) {
-    return (kt * PF_BK + PF_BK > P + qt32 * 32 - near) || (sink && kt == 0);
+// Exact-tile predicate of the reference (prefill.cu:1380-1382), stated on its
+// 64-key tiles: tile kt64 is exact for the 32-query tile qt32 iff
+// kt64*64 + 64 > P + qt32*32 - near, or sink and kt64 == 0.
+__device__ __forceinline__ bool lk_pf_exact(int P, int qt32, int kt64, int near, int sink) {
+    return (kt64 * 64 + 64 > P + qt32 * 32 - near) || (sink && kt64 == 0);
 }
 
 // The int32 S^T block of 16 keys x 16 queries over the full head_dim: A = 16
@@ -131,16 +135,32 @@ __device__ __forceinline__ lk_i4 lk_mfma_qk8(lk_i4 kfrag, lk_i4 qfrag) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(kfrag, qfrag, z, 0, 0, 0);
 }
 
+// Four fp16 of one V column from a row-major LDS tile via the gfx950 transpose
+// read.  Within each 16-lane group, lane 4a+b supplies the address of
+// V[key0 + a][dim0 + 4b .. +3]; lane c then receives V[key0 .. key0+3][dim0 + c].
+__device__ __forceinline__ lk_h4 lk_ds_tr4(const int8_t * p) {
+    typedef short lk_s4 __attribute__((ext_vector_type(4)));
+    const lk_s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) lk_s4 *) (p));
+    return __builtin_bit_cast(lk_h4, v);
+}
+
 template <bool INT8>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 2)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
              const float * __restrict__ qcs, const _Float16 * __restrict__ qh, int m, int P,
              const int8_t * __restrict__ k8, const float * __restrict__ ksc, int kstride,
              const _Float16 * __restrict__ kc, const _Float16 * __restrict__ vc,
              int near, int sink, float * __restrict__ o) {
     __shared__ PfStage st[2];
-    const int qt   = gridDim.x - 1 - blockIdx.x;        // longest rows first
+    __shared__ __attribute__((aligned(16))) int8_t s_q[4][PF_BQ * PF_Q_LD];   // fp16 Q, per head
+    // Causal work grows with the query block.  Workgroups are dispatched in
+    // linear order and the second half of the grid lands beside the first half
+    // on the CUs, so kv heads 0-3 take the query blocks longest-first and kv
+    // heads 4-7 shortest-first: co-resident workgroups then pair a long block
+    // with a short one.
     const int kvh  = blockIdx.y;
+    const int qt   = (kvh < LK_N_KV_HEADS / 2) ? (int) (gridDim.x - 1 - blockIdx.x) : (int) blockIdx.x;
     const int tid  = threadIdx.x;
     const int lane = tid & 63, w = tid >> 6;
     const int col  = lane & 15, g = lane >> 4;
@@ -151,99 +171,91 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     const int nkt = (kend + PF_BK - 1) / PF_BK;
     const int qt32_lo = qbase / 32, qt32_hi = qbase / 32 + 1;   // qb 0-1, qb 2-3
 
-    // ---- this lane's query operands (B of S^T), one per 16-query block -------
-    // The int8 fragments stay in registers; the fp16 ones are re-read (from L2)
-    // on the few exact tiles only.
+    // ---- this wave's fp16 Q block (64 rows x 128 B) into LDS, for exact tiles --
+    {
+        const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = (lane >> 3) + 8 * i, c = lane & 7;
+            const int qr = qbase + r;
+            const lk_h8 v = (qr < m) ? *(const lk_h8 *) (qh + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 8 * c) : z8;
+            *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * c) = v;
+        }
+    }
+    // ---- int8 Q operands and per-query scalars (lane column = query) ----------
     lk_i4 qf8[PF_QB];
-    float rq[PF_QB], qc[PF_QB];
-    const _Float16 * qrow[PF_QB];
+    float sq[PF_QB], isq[PF_QB], qc[PF_QB];
 #pragma unroll
     for (int qb = 0; qb < PF_QB; ++qb) {
         const int qr = qbase + 16 * qb + col;
         const bool ok = qr < m;
-        const size_t base = (size_t) (ok ? qr : 0) * LK_HIDDEN + head * LK_HEAD_DIM;
-        qrow[qb] = ok ? qh + base : nullptr;
+        const lk_i4 zi = { 0, 0, 0, 0 };
         if (INT8) {
-            const lk_i4 zi = { 0, 0, 0, 0 };
-            qf8[qb] = ok ? *(const lk_i4 *) (q8 + base + 16 * g) : zi;
-            rq[qb] = ok ? qsc[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            qf8[qb] = ok ? *(const lk_i4 *) (q8 + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 16 * g) : zi;
+            const float d = ok ? qsc[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            // scores are kept in units of 1/sq until the exponent (sq > 0 scales
+            // commute with the max); an all-zero query row has sq = 0 and zero
+            // int8 scores, so unit scaling is exact for it
+            sq[qb] = (d > 0.0f) ? d : 1.0f;
+            isq[qb] = 1.0f / sq[qb];
             qc[qb] = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
         } else {
-            rq[qb] = 0.0f; qc[qb] = 0.0f;
+            qf8[qb] = zi; sq[qb] = 1.0f; isq[qb] = 1.0f; qc[qb] = 0.0f;
         }
     }
 
     // ---- tile staging: global -> registers -> LDS ------------------------------
-    // K8: thread t -> key t/4, 16-byte chunk t%4.   Kh: two 16-byte chunks,
-    // ids t and t+256 -> key id/8, chunk id%8.   V: key pair t/8 (keys 2p, 2p+1),
-    // dims 8*(t%8)..+7, written transposed as 8 packed (key 2p, key 2p+1) words.
-    lk_i4 rk8;
-    lk_h8 rkh[2], rv[2];
-    float4 rks;
-    const int kp8 = tid >> 2, c8 = tid & 3;
-    const int vkp = tid >> 3, vc8 = tid & 7;
+    // K8: threads 0..127 -> key t/4, 16-byte chunk t%4; threads 128..135 the
+    // 32 scales.  Kh and V: every thread one 16-byte chunk, key t/8, chunk t%8.
+    lk_i4 rk8, rkh, rv;
     const float * ks_h = INT8 ? ksc + (size_t) kvh * kstride : nullptr;
-
-    auto tile_needs_exact = [&](int kt) {
-        return !INT8 || lk_pf_exact(P, qt32_lo, kt, near, sink);
-    };
-    auto tile_needs_int8 = [&](int kt) {
-        return INT8 && !lk_pf_exact(P, qt32_hi, kt, near, sink);
+    auto tile_exact = [&](int kt, int qt32) {
+        return !INT8 || lk_pf_exact(P, qt32, (kt * PF_BK) / 64, near, sink);
     };
     auto load_regs = [&](int kt) {
         const int kb0 = kt * PF_BK;
-        const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
-        if (tile_needs_int8(kt)) {
-            const int kpos = kb0 + kp8;
-            const lk_i4 zi = { 0, 0, 0, 0 };
-            rk8 = (kpos < kend) ? *(const lk_i4 *) (k8 + ((size_t) kpos * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 16 * c8) : zi;
-            if (tid < 16) {
-                const int sp = kb0 + 4 * tid;
-                rks = (sp < kend) ? *(const float4 *) (ks_h + sp) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const lk_i4 zi = { 0, 0, 0, 0 };
+        if (INT8 && !tile_exact(kt, qt32_hi)) {
+            if (tid < 128) {
+                const int kpos = kb0 + (tid >> 2);
+                rk8 = (kpos < kend) ? *(const lk_i4 *) (k8 + ((size_t) kpos * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 16 * (tid & 3)) : zi;
+            } else if (tid < 136) {
+                const int sp = kb0 + 4 * (tid - 128);
+                rk8 = (sp < kend) ? *(const lk_i4 *) (ks_h + sp) : zi;
             }
         }
-        if (tile_needs_exact(kt)) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int id = tid + 256 * i;
-                const int kpos = kb0 + (id >> 3);
-                rkh[i] = (kpos < kend) ? *(const lk_h8 *) (kc + ((size_t) kpos * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 8 * (id & 7)) : z8;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int kpos = kb0 + 2 * vkp + i;
-            rv[i] = (kpos < kend) ? *(const lk_h8 *) (vc + ((size_t) kpos * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 8 * vc8) : z8;
-        }
+        const int kpos = kb0 + (tid >> 3);
+        const size_t goff = ((size_t) kpos * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 8 * (tid & 7);
+        if (tile_exact(kt, qt32_lo))
+            rkh = (kpos < kend) ? *(const lk_i4 *) (kc + goff) : zi;
+        rv = (kpos < kend) ? *(const lk_i4 *) (vc + goff) : zi;
     };
     auto store_lds = [&](int kt, PfStage & S) {
-        if (tile_needs_int8(kt)) {
-            *(lk_i4 *) (S.k8 + kp8 * PF_K8_LD + 16 * c8) = rk8;
-            if (tid < 16) *(float4 *) (S.ks + 4 * tid) = rks;
+        if (INT8 && !tile_exact(kt, qt32_hi)) {
+            if (tid < 128) *(lk_i4 *) (S.k8 + (tid >> 2) * PF_K8_LD + 16 * (tid & 3)) = rk8;
+            else if (tid < 136) *(lk_i4 *) (S.ks + 4 * (tid - 128)) = rk8;
         }
-        if (tile_needs_exact(kt)) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int id = tid + 256 * i;
-                *(lk_h8 *) (S.kh + (id >> 3) * PF_KH_LD + 8 * (id & 7)) = rkh[i];
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-            h2 pr = { rv[0][e], rv[1][e] };
-            *(h2 *) (S.vt + (8 * vc8 + e) * PF_VT_LD + 2 * vkp) = pr;
-        }
+        if (tile_exact(kt, qt32_lo)) *(lk_i4 *) (S.kh + (tid >> 3) * PF_KH_LD + 16 * (tid & 7)) = rkh;
+        *(lk_i4 *) (S.v + (tid >> 3) * PF_V_LD + 16 * (tid & 7)) = rv;
     };
 
-    lk_f4 acc[4][PF_QB];                    // O^T blocks [dim block][query block]
+    // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
+    // all-ones A operand, so every lane of query column q accumulates
+    // l_q = sum of the same fp16 P the numerator uses.
+    lk_f4 acc[5][PF_QB];
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 5; ++db)
 #pragma unroll
         for (int qb = 0; qb < PF_QB; ++qb) acc[db][qb] = (lk_f4){ 0.f, 0.f, 0.f, 0.f };
-    float mrun[PF_QB], lrun[PF_QB];
+    float mrun[PF_QB];                      // running max, units of 1/sq
 #pragma unroll
-    for (int qb = 0; qb < PF_QB; ++qb) { mrun[qb] = -INFINITY; lrun[qb] = 0.0f; }
+    for (int qb = 0; qb < PF_QB; ++qb) mrun[qb] = -INFINITY;
+    const _Float16 one = (_Float16) 1.0f;
+    const lk_h8 ones = { one, one, one, one, one, one, one, one };
+    // The running max is only raised when a score exceeds it by more than
+    // 2^PF_HEADROOM in p (so most tiles skip the rescale); p <= 2^8 stays far
+    // inside fp16 range and loses no relative precision.
+    constexpr float PF_HEADROOM = 8.0f;
 
     load_regs(0);
     store_lds(0, st[0]);
@@ -253,42 +265,41 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         if (kt + 1 < nkt) load_regs(kt + 1);
         const PfStage & S = st[kt & 1];
         const int kb0 = kt * PF_BK;
-        const bool ex_lo = !INT8 || lk_pf_exact(P, qt32_lo, kt, near, sink);
-        const bool ex_hi = !INT8 || lk_pf_exact(P, qt32_hi, kt, near, sink);
+        const bool ex_lo = tile_exact(kt, qt32_lo);
+        const bool ex_hi = tile_exact(kt, qt32_hi);
 
-        // ---- scores S^T[kb][qb] (keys 16kb+4g+r, query 16qb+col) ----------------
-        float s[4][PF_QB][4];
+        // ---- scores S^T[kb][qb] (keys kb0+16kb+4g+r, query 16qb+col), x-units ----
+        float x[2][PF_QB][4];
         if (ex_lo) {
-            // fp16 K fragments of the tile (A operand), 2 k-steps of 32 dims
-            lk_h8 ka[4][2];
+            lk_h8 ka[2][2];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks)
-                    ka[kb][ks] = *(const lk_h8 *) (S.kh + (16 * kb + col) * PF_KH_LD + 32 * ks + 8 * g);
+                    ka[kb][ks] = *(const lk_h8 *) (S.kh + (16 * kb + col) * PF_KH_LD + 64 * ks + 16 * g);
 #pragma unroll
             for (int qb = 0; qb < PF_QB; ++qb) {
                 const bool ex = (qb < 2) ? ex_lo : ex_hi;
                 if (!ex) continue;
-                const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
-                const lk_h8 qf0 = qrow[qb] ? *(const lk_h8 *) (qrow[qb] + 8 * g) : z8;
-                const lk_h8 qf1 = qrow[qb] ? *(const lk_h8 *) (qrow[qb] + 32 + 8 * g) : z8;
+                const int8_t * qrow = s_q[w] + (16 * qb + col) * PF_Q_LD + 16 * g;
+                const lk_h8 qf0 = *(const lk_h8 *) qrow;
+                const lk_h8 qf1 = *(const lk_h8 *) (qrow + 64);
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
+                for (int kb = 0; kb < 2; ++kb) {
                     lk_f4 c = { 0.f, 0.f, 0.f, 0.f };
                     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kb][0], qf0, c, 0, 0, 0);
                     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kb][1], qf1, c, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        s[kb][qb][r] = INT8 ? fmaf(c[r], LK_LOG2E_F, -qc[qb]) : c[r] * LK_LOG2E_F;
+                        x[kb][qb][r] = INT8 ? fmaf(c[r], LK_LOG2E_F, -qc[qb]) * isq[qb] : c[r] * LK_LOG2E_F;
                 }
             }
         }
         if (INT8 && !ex_hi) {
-            lk_i4 ka8[4];
-            float4 skv[4];
+            lk_i4 ka8[2];
+            float4 skv[2];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
+            for (int kb = 0; kb < 2; ++kb) {
                 ka8[kb] = *(const lk_i4 *) (S.k8 + (16 * kb + col) * PF_K8_LD + 16 * g);
                 skv[kb] = *(const float4 *) (S.ks + 16 * kb + 4 * g);
             }
@@ -297,12 +308,12 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 const bool ex = (qb < 2) ? ex_lo : ex_hi;
                 if (ex) continue;
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
+                for (int kb = 0; kb < 2; ++kb) {
                     const lk_i4 c = lk_mfma_qk8(ka8[kb], qf8[qb]);
-                    s[kb][qb][0] = (float) c[0] * skv[kb].x * rq[qb];
-                    s[kb][qb][1] = (float) c[1] * skv[kb].y * rq[qb];
-                    s[kb][qb][2] = (float) c[2] * skv[kb].z * rq[qb];
-                    s[kb][qb][3] = (float) c[3] * skv[kb].w * rq[qb];
+                    x[kb][qb][0] = (float) c[0] * skv[kb].x;
+                    x[kb][qb][1] = (float) c[1] * skv[kb].y;
+                    x[kb][qb][2] = (float) c[2] * skv[kb].z;
+                    x[kb][qb][3] = (float) c[3] * skv[kb].w;
                 }
             }
         }
@@ -313,62 +324,56 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             for (int qb = 0; qb < PF_QB; ++qb) {
                 const int qpos = P + qbase + 16 * qb + col;
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
+                for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (kb0 + 16 * kb + 4 * g + r > qpos) s[kb][qb][r] = -INFINITY;
+                        if (kb0 + 16 * kb + 4 * g + r > qpos) x[kb][qb][r] = -INFINITY;
             }
         }
 
-        // ---- online softmax (log2 domain), per query = per lane column ----------
+        // ---- online softmax, per query (lane column); exponent = sq * (x - m) ---
 #pragma unroll
         for (int qb = 0; qb < PF_QB; ++qb) {
-            float mx = s[0][qb][0];
+            float mx = fmaxf(fmaxf(fmaxf(x[0][qb][0], x[0][qb][1]), fmaxf(x[0][qb][2], x[0][qb][3])),
+                             fmaxf(fmaxf(x[1][qb][0], x[1][qb][1]), fmaxf(x[1][qb][2], x[1][qb][3])));
+            mx = lk_xrow_max(mx);
+            // key 0 is visible to every query, so mrun is finite after tile 0
+            const bool need = mx > mrun[qb] + PF_HEADROOM * isq[qb];
+            if (__ballot(need)) {                              // wave-uniform branch
+                const float alpha = need ? lk_exp2((mrun[qb] - mx) * sq[qb]) : 1.0f;
+                mrun[qb] = need ? mx : mrun[qb];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
+                for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
+            }
+            const float msq = mrun[qb] * sq[qb];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][qb][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(mrun[qb], mx);      // finite: key 0 is always visible
-            const float alpha = lk_exp2(mrun[qb] - mnew);
-            mrun[qb] = mnew;
-            float ls = 0.0f;
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float p = lk_exp2(s[kb][qb][r] - mnew);
-                    s[kb][qb][r] = p;
-                    ls += p;
-                }
-            lrun[qb] = lrun[qb] * alpha + ls;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db][qb] *= alpha;
+                for (int r = 0; r < 4; ++r) x[kb][qb][r] = lk_exp2(fmaf(x[kb][qb][r], sq[qb], -msq));
         }
 
-        // ---- O^T += V^T . P^T ---------------------------------------------------
+        // ---- O^T += V^T . P^T over the 32 keys -----------------------------------
+        lk_h8 pb[PF_QB];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            lk_h8 pb[PF_QB];
+        for (int qb = 0; qb < PF_QB; ++qb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pb[qb][r]     = (_Float16) x[0][qb][r];
+                pb[qb][4 + r] = (_Float16) x[1][qb][r];
+            }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int8_t * vp = S.v + (col >> 2) * PF_V_LD + 2 * (16 * db + 4 * (col & 3));
+            const lk_h4 lo = lk_ds_tr4(vp + (4 * g) * PF_V_LD);
+            const lk_h4 hi = lk_ds_tr4(vp + (16 + 4 * g) * PF_V_LD);
+            const lk_h8 va = { lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3] };
 #pragma unroll
             for (int qb = 0; qb < PF_QB; ++qb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    pb[qb][r]     = (_Float16) s[2 * ks][qb][r];
-                    pb[qb][4 + r] = (_Float16) s[2 * ks + 1][qb][r];
-                }
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const _Float16 * vrow = S.vt + (16 * db + col) * PF_VT_LD + 32 * ks + 4 * g;
-                const lk_h4 lo = *(const lk_h4 *) vrow;
-                const lk_h4 hi = *(const lk_h4 *) (vrow + 16);
-                const lk_h8 va = { lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3] };
-#pragma unroll
-                for (int qb = 0; qb < PF_QB; ++qb)
-                    acc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qb], acc[db][qb], 0, 0, 0);
-            }
+                acc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qb], acc[db][qb], 0, 0, 0);
         }
+#pragma unroll
+        for (int qb = 0; qb < PF_QB; ++qb)
+            acc[4][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[qb], acc[4][qb], 0, 0, 0);
 
         if (kt + 1 < nkt) store_lds(kt + 1, st[(kt + 1) & 1]);
         __syncthreads();
@@ -377,10 +382,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // ---- epilogue: l over the 4 lane groups, then o[q][head*64 + d] -------------
 #pragma unroll
     for (int qb = 0; qb < PF_QB; ++qb) {
-        float l = lrun[qb];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
-        const float il = 1.0f / l;
+        const float il = 1.0f / acc[4][qb][0];
         const int qr = qbase + 16 * qb + col;
         if (qr < m) {
 #pragma unroll
