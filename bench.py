@@ -31,6 +31,18 @@ PEAK_FP16_TFLOPS = 2500.0             # dense fp16 MFMA
 REF_3090TI_GBS_32K = 669.3            # reference, RTX 3090 Ti, docs/ARCHITECTURE.md:2401
 
 
+def split_traffic_from_profile():
+    """HBM bytes per C2 split launch, from the committed rocprofv3 FETCH_SIZE +
+    WRITE_SIZE summary (calibrated against a 1 GiB copy), or None."""
+    import re
+    try:
+        txt = open(os.path.join(ROOT, "profiles", "decode_attn_c2_c3.md")).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch = (\d+)", txt)
+    return int(m.group(1)) if m else None
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -209,6 +221,27 @@ def cpu_baseline(seconds):
     return res
 
 
+def profile_decode_split(lk, lkc, launches):
+    """For rocprofv3 --pmc runs: `launches` back-to-back lk_attn_split launches
+    on C2 (rotating over 10 distinct 67 MB caches), then one 1 GiB device copy
+    whose FETCH_SIZE / WRITE_SIZE calibrate the counters (it reads and writes
+    exactly 2^30 bytes)."""
+    import torch
+    qs, kcs, vcs, seq = lkc.decode_inputs("C2", layers=10)
+    d_pos = torch.tensor([seq - 1], dtype=torch.int32, device="cuda")
+    part = torch.empty(lk.part_bytes() // 4, device="cuda")
+    for i in range(launches):
+        lk.attn_split(qs[i % 10], kcs[i % 10], vcs[i % 10], d_pos, part)
+    torch.cuda.synchronize()
+    src = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"profile: {launches} split launches (C2, seq {seq}, {seq * 2048} algorithmic bytes each), "
+        f"then a {src.numel() * 4} byte copy")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -218,6 +251,8 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile-split", type=int, default=0,
+                    help="only run N C2 split launches + a 1 GiB copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this attention path is built and measured on a single "
@@ -230,6 +265,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     lk.load()
     cfgp = lk.config()
+    if args.profile_split:
+        profile_decode_split(lk, lkc, args.profile_split)
+        return
 
     log("decode C2 (32k x 10 layers, one hipGraph)")
     c2 = bench_decode(lk, lkc, "C2", args.steps, args.warmup, args.kernel_iters)
@@ -278,7 +316,7 @@ def main():
             "baseline": "reference on RTX 3090 Ti: 669.3 GB/s, 100.27 us/layer @32768",
         },
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": split_traffic_from_profile(),
                      "kernel": "lk_k_attn_split (C2, seq x 2048 B per launch)"},
         "cpu_baseline": cpu,
         "results": results,
