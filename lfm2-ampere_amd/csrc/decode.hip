@@ -139,90 +139,103 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
     for (int i = 0; i < D; ++i)
         if (i < ntile) fetch(i);
 
-    // A operand: row i = col carries query head 4w + (i & 3); k-slots 8g..8g+7
-    // of MFMA 0 are dims 16g..16g+7, of MFMA 1 dims 16g+8..16g+15 -- the same
-    // dims this lane reads of its token, so A and B agree slot by slot.
-    lk_h8 qa0h, qa0l, qa1h, qa1l;
+    // Scores are computed transposed, S^T = K . Q^T (v_mfma_f32_16x16x32_f16):
+    // A = 16 cache rows of the tile (lane: position col, dims 32ks+8g..+7),
+    // B = Q^T with the 4 heads of kv head w replicated over the 16 columns
+    // (column c = head 4w + (c & 3)).  Lane l then holds positions 4g..4g+3 of
+    // one head, which is exactly the B operand of the P.V MFMA.  q is fp32 in
+    // the interface: split q = hi + lo (fp16 x fp16 products are exact in fp32)
+    // and both halves are multiplied.
+    lk_h8 qbh[2], qbl[2];
     {
-        const float * qp = q + (w * LK_G + (col & 3)) * LK_HEAD_DIM + 16 * g;
+        const float * qp = q + (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            _Float16 h, l;
-            lk_split_h(qp[i], h, l);     qa0h[i] = h; qa0l[i] = l;
-            lk_split_h(qp[8 + i], h, l); qa1h[i] = h; qa1l[i] = l;
-        }
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                _Float16 h, l;
+                lk_split_h(qp[32 * ks + i], h, l);
+                qbh[ks][i] = h; qbl[ks][i] = l;
+            }
     }
     const float SC = 0.125f * LK_LOG2E_F;      // scores in log2 units
+    // Running max is raised only when a score exceeds it by 2^8 in p: P stays
+    // far inside fp16 range and most tiles skip the rescale.
+    constexpr float HEADROOM = 8.0f;
 
-    float mrun[4], lrun[4], acc[4][16];
+    float mrun = -INFINITY;
+    lk_f4 acc[4], accl;                     // O^T blocks (dims 16db..) and sum of p
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        mrun[r] = -1e30f; lrun[r] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) acc[r][k] = 0.0f;
-    }
+    for (int db = 0; db < 4; ++db) acc[db] = (lk_f4){ 0.f, 0.f, 0.f, 0.f };
+    accl = (lk_f4){ 0.f, 0.f, 0.f, 0.f };
+    const _Float16 one = (_Float16) 1.0f;
+    const lk_h4 ones = { one, one, one, one };
 
-    // ---- consume one tile: wave w = kv head w, NG groups of 16 tokens --------
+    // ---- consume one tile: wave w = kv head w, NG blocks of 16 positions -----
     auto consume = [&](const unsigned char * buf, int it) {
 #if LK_DEC_ABLATE == 3
-        if (buf[lane] == 0x7f && it < 0) lrun[0] += 1.0f;
+        if (buf[lane] == 0x7f && it < 0) accl[0] += 1.0f;
         return;
 #endif
-        float s[NG][4];
-        float mloc[4] = { -INFINITY, -INFINITY, -INFINITY, -INFINITY };
+        float x[NG][4];
+        float mloc = -INFINITY;
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
-            const unsigned char * kr = buf + (16 * gi + col) * LK_DEC_ROWB + w * 128 + 32 * g;
+            const unsigned char * kr = buf + (16 * gi + col) * LK_DEC_ROWB + w * 128 + 16 * g;
             lk_f4 c = { 0.0f, 0.0f, 0.0f, 0.0f };
 #if LK_DEC_ABLATE == 2
-            s[gi][0] = s[gi][1] = s[gi][2] = s[gi][3] = (float) col;
-            continue;
-#endif
+            c[0] = c[1] = c[2] = c[3] = (float) col;
+#else
             const lk_h8 k0 = *(const lk_h8 *) kr;
-            const lk_h8 k1 = *(const lk_h8 *) (kr + 16);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa0h, k0, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa0l, k0, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa1h, k1, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa1l, k1, c, 0, 0, 0);
-            const bool ok = it * LK_DEC_TILE + 16 * gi + col < n;
+            const lk_h8 k1 = *(const lk_h8 *) (kr + 64);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qbh[0], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qbl[0], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qbh[1], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qbl[1], c, 0, 0, 0);
+#endif
+            const int t0g = it * LK_DEC_TILE + 16 * gi + 4 * g;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                s[gi][r] = ok ? c[r] * SC : -INFINITY;
-                mloc[r] = fmaxf(mloc[r], s[gi][r]);
+                x[gi][r] = (t0g + r < n) ? c[r] * SC : -INFINITY;
+                mloc = fmaxf(mloc, x[gi][r]);
             }
         }
+        // every lane of a column (and its 3 replicas) sees the same max
+        const float mx = lk_xrow_max(mloc);
+        const bool need = mx > mrun + HEADROOM;
+        if (__ballot(need)) {                                   // wave-uniform
+            const float alpha = need ? lk_exp2(mrun - mx) : 1.0f;
+            mrun = need ? mx : mrun;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float mnew = fmaxf(mrun[r], lk_row_max16(mloc[r]));
-            // every lane holds the same mnew (rows replicate the same tokens),
-            // so this branch is wave-uniform; most tiles do not raise the max
-            if (mnew > mrun[r]) {
-                const float alpha = lk_exp2(mrun[r] - mnew);
-                mrun[r] = mnew;
-                lrun[r] *= alpha;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) acc[r][k] *= alpha;
-            }
+            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+            accl *= alpha;
         }
 #pragma unroll
         for (int gi = 0; gi < NG; ++gi) {
-            const unsigned char * vr = buf + (LK_DEC_TILE + 16 * gi + col) * LK_DEC_ROWB + w * 128 + 32 * g;
-#if LK_DEC_ABLATE == 1
-            lrun[0] += s[gi][0];
-            continue;
-#endif
-            const lk_h8 v0 = *(const lk_h8 *) vr;
-            const lk_h8 v1 = *(const lk_h8 *) (vr + 16);
+            lk_h4 ph, pl;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = lk_exp2(s[gi][r] - mrun[r]);
-                lrun[r] += p;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    acc[r][k]     += p * (float) v0[k];
-                    acc[r][8 + k] += p * (float) v1[k];
-                }
+                const float p = lk_exp2(x[gi][r] - mrun);
+                ph[r] = (_Float16) p;
+                pl[r] = (_Float16) (p - (float) ph[r]);
             }
+#if LK_DEC_ABLATE == 1
+            accl[0] += (float) ph[0];
+            continue;
+#endif
+            // V^T operand by transpose read: lane 4a+b of row group g supplies
+            // V[position 4g+a][dims 16db+4b..+3]; lane c receives the 4
+            // positions 4g..4g+3 of dim 16db + c.
+            const unsigned char * vr = buf + (LK_DEC_TILE + 16 * gi + 4 * g + (col >> 2)) * LK_DEC_ROWB
+                                     + w * 128 + 8 * (col & 3);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const lk_h4 va = lk_ds_tr4(vr + 32 * db);
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, acc[db], 0, 0, 0);
+                acc[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, acc[db], 0, 0, 0);
+            }
+            accl = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, ph, accl, 0, 0, 0);
+            accl = __builtin_amdgcn_mfma_f32_16x16x16f16(ones, pl, accl, 0, 0, 0);
         }
     };
 
@@ -234,28 +247,13 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
         if (it + D < ntile) fetch(it + D);
     }
 
-    // Sum the 16 token lanes of each row (fixed DPP butterfly): afterwards
-    // every lane of row group g holds l and acc for dims 16g..16g+15.
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        lrun[r] = lk_row_sum16(lrun[r]);
-#pragma unroll
-        for (int k = 0; k < 16; ++k) acc[r][k] = lk_row_sum16(acc[r][k]);
-    }
-    // Partial record of query head 4w + r: lane col == r of row group g writes
-    // dims 16g..16g+15 (as four 16-byte stores); lane 0 of the row writes m, l.
+    // Partial record of query head 4w + c, written by the lanes of columns
+    // c = 0..3: O^T rows 16db + 4g + r; the sum of p is in every row of accl.
     if (col < 4) {
-        const int r = col;
-        float * P = part + ((size_t) (w * LK_G + r) * LK_ATTN_SPLIT + sp) * LK_ATTN_PARTW;
-        float a[16];
+        float * P = part + ((size_t) (w * LK_G + col) * LK_ATTN_SPLIT + sp) * LK_ATTN_PARTW;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) a[k] = (r == 0) ? acc[0][k] : (r == 1) ? acc[1][k] : (r == 2) ? acc[2][k] : acc[3][k];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) P[4 + 16 * g + k] = a[k];
-        if (g == 0) {
-            P[0] = (r == 0) ? mrun[0] : (r == 1) ? mrun[1] : (r == 2) ? mrun[2] : mrun[3];
-            P[1] = (r == 0) ? lrun[0] : (r == 1) ? lrun[1] : (r == 2) ? lrun[2] : lrun[3];
-        }
+        for (int db = 0; db < 4; ++db) *(lk_f4 *) (P + 4 + 16 * db + 4 * g) = acc[db];
+        if (g == 0) { P[0] = mrun; P[1] = accl[0]; }
     }
 }
 

@@ -96,6 +96,21 @@ __device__ __forceinline__ float lk_xrow_max(float x) {
 __device__ __forceinline__ float lk_xrow_max(float x) { return x; }
 #endif
 
+// Four fp16 of one column from a row-major LDS tile via the gfx950 transpose
+// read (ds_read_b64_tr_b16).  Within each 16-lane group, lane 4a+b supplies
+// the address of T[row0 + a][col0 + 4b .. +3]; lane c then receives
+// T[row0 .. row0+3][col0 + c].
+#ifdef __HIP_DEVICE_COMPILE__
+__device__ __forceinline__ lk_h4 lk_ds_tr4(const void * p) {
+    typedef short lk_s4 __attribute__((ext_vector_type(4)));
+    const lk_s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) lk_s4 *) (p));
+    return __builtin_bit_cast(lk_h4, v);
+}
+#else
+__device__ __forceinline__ lk_h4 lk_ds_tr4(const void *) { return lk_h4{}; }
+#endif
+
 // 2^x on the transcendental unit (v_exp_f32); 2^-inf = 0.
 __device__ __forceinline__ float lk_exp2(float x) {
 #if defined(__HIP_DEVICE_COMPILE__)

@@ -135,16 +135,6 @@ __device__ __forceinline__ lk_i4 lk_mfma_qk8(lk_i4 kfrag, lk_i4 qfrag) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(kfrag, qfrag, z, 0, 0, 0);
 }
 
-// Four fp16 of one V column from a row-major LDS tile via the gfx950 transpose
-// read.  Within each 16-lane group, lane 4a+b supplies the address of
-// V[key0 + a][dim0 + 4b .. +3]; lane c then receives V[key0 .. key0+3][dim0 + c].
-__device__ __forceinline__ lk_h4 lk_ds_tr4(const int8_t * p) {
-    typedef short lk_s4 __attribute__((ext_vector_type(4)));
-    const lk_s4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) lk_s4 *) (p));
-    return __builtin_bit_cast(lk_h4, v);
-}
-
 template <bool INT8>
 __global__ void __launch_bounds__(256, 2)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
