@@ -300,77 +300,91 @@ __device__ __forceinline__ void lk_quant_q8_1_half(float x, lk_block_q8_1 * __re
     }
 }
 
-// Combine: grid (32 query heads, 2 halves of the 64 dims), 256 threads, one
-// slice per thread.  Slices s with s*chunk >= seq hold no tokens and are
-// skipped (reference kernels.cu:1573-1584).  Each thread requests its slice's
-// (m, l) and 32 acc values at once (one memory round trip), the block max M is
-// exact, the slice weights are 2^(m_s - M), and the weighted values are summed
-// in a fixed order: 8 segments of 32 consecutive slices serially, then the 8
-// segment sums in index order.  Fixed order => bit-reproducible output.  Each
-// half is exactly one Q8_1 block of the next GEMV's input.
-static_assert(LK_ATTN_SPLIT <= 256 && LK_ATTN_SPLIT % 32 == 0, "combine assumes <= 256 slices");
-__device__ __forceinline__ float lk_wave_max(float v) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+// Combine: grid (32 query heads, 2 halves of the 64 dims), 256 threads.
+// Slices s with s*chunk >= seq hold no tokens and are skipped (reference
+// kernels.cu:1573-1584).  Every lane requests its slices' (m, l) and values at
+// once (one memory round trip), the max M is exact, the slice weights are
+// 2^(m_s - M).  Each half is exactly one Q8_1 block of the next GEMV's input.
+// Sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the gfx950
+// lane swaps; like lk_xrow_max, every lane ends with identical bits.
+#ifdef __HIP_DEVICE_COMPILE__
+__device__ __forceinline__ float lk_xrow_sum(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    float c = a + b, d = c;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
+    return c + d;
 }
+#else
+__device__ __forceinline__ float lk_xrow_sum(float x) { return x; }
+#endif
 
+// Combine: workgroup (head, half) produces 32 output dims; wave w owns dims
+// 32*half + 8w .. +7 over all slices, lane l the slices l, l+64, l+128, l+192.
+// Every sum runs in a fixed order (per lane in slice order, then a fixed
+// lane tree), so the output is run-to-run bit-identical.
+static_assert(LK_ATTN_SPLIT <= 256, "combine: at most 4 slices per lane");
 __global__ void __launch_bounds__(256)
 lk_k_attn_combine(const float * __restrict__ part, const int * __restrict__ d_pos,
                   float * __restrict__ out, lk_block_q8_1 * __restrict__ yq8) {
+    constexpr int J = (LK_ATTN_SPLIT + 63) / 64;
     const int head = blockIdx.x, half = blockIdx.y;
     const int seq = *d_pos + 1;
     int ns, chunk;
     lk_attn_slices(seq, ns, chunk);
     const int nv = (seq + chunk - 1) / chunk;        // non-empty slices, <= ns
-    const int s = threadIdx.x, lane = s & 63, wv = s >> 6;
-    const bool live = s < nv;
-    const float * R = part + ((size_t) head * LK_ATTN_SPLIT + (live ? s : 0)) * LK_ATTN_PARTW;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int d0 = 32 * half + 8 * wv;
 
-    lk_f4 a[8];
+    float m[J], l[J];
+    lk_f4 a0[J], a1[J];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) a[i] = *(const lk_f4 *) (R + 4 + 32 * half + 4 * i);
-    const lk_f4 ml = *(const lk_f4 *) R;             // m, l, pad, pad
-    const float m = live ? ml[0] : -1e30f;
-
-    __shared__ float s_red[4];
-    __shared__ float s_v[256][33];                   // weighted values, col 32 = l*w
-    __shared__ float s_seg[8][33];
-    const float mx = lk_wave_max(m);
-    if (lane == 0) s_red[wv] = mx;
-    __syncthreads();
-    const float M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    const float wgt = live ? lk_exp2(m - M) : 0.0f;
+    for (int j = 0; j < J; ++j) {
+        const int s = lane + 64 * j;
+        const bool live = s < nv;
+        const float * R = part + ((size_t) head * LK_ATTN_SPLIT + (live ? s : 0)) * LK_ATTN_PARTW;
+        const lk_f4 ml = *(const lk_f4 *) R;         // m, l, pad, pad
+        a0[j] = *(const lk_f4 *) (R + 4 + d0);
+        a1[j] = *(const lk_f4 *) (R + 8 + d0);
+        m[j] = live ? ml[0] : -1e30f;
+        l[j] = live ? ml[1] : 0.0f;
+    }
+    float M = m[0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int j = 1; j < J; ++j) M = fmaxf(M, m[j]);
+    M = lk_xrow_max(lk_row_max16(M));
+    float L = 0.0f;
+    lk_f4 A0 = { 0.f, 0.f, 0.f, 0.f }, A1 = A0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) s_v[s][4 * i + k] = a[i][k] * wgt;
-    s_v[s][32] = live ? ml[1] * wgt : 0.0f;
-    __syncthreads();
-    // 8 segments x 33 columns: thread (column c, segment j) sums 32 slices in order
-    {
-        const int c = s & 63, j = s >> 6;           // c < 33 used; j = 0..3 covers 2 segments each
-        if (c < 33) {
+    for (int j = 0; j < J; ++j) {
+        const float e = lk_exp2(m[j] - M);           // dead slices: exp2(-1e30 - M) = 0
+        L += l[j] * e;
+        A0 += a0[j] * e;
+        A1 += a1[j] * e;
+    }
+    L = lk_xrow_sum(lk_row_sum16(L));
+    float o[8];
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const int seg = 2 * j + jj;
-                float t = 0.0f;
-#pragma unroll 8
-                for (int i = 0; i < 32; ++i) t += s_v[32 * seg + i][c];
-                s_seg[seg][c] = t;
-            }
+    for (int k = 0; k < 4; ++k) {
+        o[k]     = lk_xrow_sum(lk_row_sum16(A0[k]));
+        o[4 + k] = lk_xrow_sum(lk_row_sum16(A1[k]));
+    }
+    const float il = 1.0f / L;
+    __shared__ float s_o[32];
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            o[k] *= il;
+            s_o[8 * wv + k] = o[k];
+        }
+        if (out) {
+            *(lk_f4 *) (out + head * LK_HEAD_DIM + d0)     = (lk_f4){ o[0], o[1], o[2], o[3] };
+            *(lk_f4 *) (out + head * LK_HEAD_DIM + d0 + 4) = (lk_f4){ o[4], o[5], o[6], o[7] };
         }
     }
+    if (!yq8) return;                                 // workgroup-uniform
     __syncthreads();
-    if (wv == 0) {
-        const int c = lane & 31;
-        float A = 0.0f, L = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) { A += s_seg[j][c]; L += s_seg[j][32]; }
-        const float o = A * (1.0f / L);
-        if (out && lane < 32) out[head * LK_HEAD_DIM + 32 * half + c] = o;
-        if (yq8) lk_quant_q8_1_half(o, yq8 + 2 * head + half);
-    }
+    if (wv == 0) lk_quant_q8_1_half(s_o[lane & 31], yq8 + 2 * head + half);
 }
 
 // Serial cross-check (reference kernels.cu:768-852): one workgroup per query
