@@ -56,29 +56,6 @@ __device__ __forceinline__ void lk_split_h(float x, _Float16 & hi, _Float16 & lo
 #define LK_DEC_ABLATE 0
 #endif
 
-// Byte address of an LDS object (the value M0 takes for an LDS DMA).
-__device__ __forceinline__ uint32_t lk_lds_addr(const void * p) {
-    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) p;
-}
-// One LDS DMA: each lane's 16 bytes at `src` land at LDS byte lds + 16*lane,
-// non-temporal (the KV stream is read once).  Issued as inline asm so the
-// compiler does not serialise later LDS reads on it; completion is tracked by
-// hand with vmcnt (in-order) plus a barrier.  M0 is written here; nothing else
-// in the decode kernels uses M0, so clobbering it is safe.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lk_dma16(const void * src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
-                 :: "v"(src), "s"(lds) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void lk_wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
 __global__ void __launch_bounds__(LK_DEC_THREADS)
 lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
                 const _Float16 * __restrict__ vc, const int * __restrict__ d_pos,

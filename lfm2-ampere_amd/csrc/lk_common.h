@@ -128,6 +128,41 @@ __host__ __device__ __forceinline__ void lk_attn_slices(int seq, int & ns, int &
     chunk = (seq + s - 1) / s;
 }
 
+// Makes a register value opaque to the optimiser (no code is emitted), so
+// values derived from it are not hoisted out of the enclosing loop.
+template <typename T>
+__device__ __forceinline__ void lk_launder(T & v) { asm volatile("" : "+v"(v)); }
+
+// ---- LDS DMA (global_load_lds_dwordx4) --------------------------------------
+// Byte address of an LDS object (the value M0 takes for an LDS DMA).
+__device__ __forceinline__ uint32_t lk_lds_addr(const void * p) {
+    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) void *) p;
+}
+// One LDS DMA: each active lane's 16 bytes at `src` land at LDS byte
+// lds + 16*lane (lds must be wave-uniform).  Issued as inline asm so the
+// compiler does not serialise later LDS reads on it; completion is tracked by
+// hand with vmcnt (in-order) plus a barrier.  M0 is written here; no other
+// code in this library uses M0, so clobbering it is safe.  lk_dma16 is
+// non-temporal (streams read once), lk_dma16c keeps the normal cache policy
+// (tiles that other workgroups read again).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lk_dma16(const void * src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :: "v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void lk_dma16c(const void * src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void lk_wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
 // ---- host-side error plumbing (lk_host.cpp) -----------------------------------
 int lk_fail(int code, const char * fmt, ...);
 // hipGetLastError after a launch, mapped into lk_fail.

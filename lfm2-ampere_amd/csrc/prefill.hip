@@ -105,20 +105,33 @@ lk_k_pf_kmean(const _Float16 * __restrict__ kc, int n, float * __restrict__ cm) 
 
 // ---------------------------------------------------------------------------
 // Flash attention.
-#define PF_BQ      64                     // query rows per workgroup (16 per block)
-#define PF_BK      32                     // keys per tile (two 16-key blocks)
+#define PF_BQ      64                     // query rows per workgroup (4 blocks of 16)
+#define PF_BK      64                     // keys per tile = the reference's 64-key tile
 #define PF_QB      (PF_BQ / 16)
-#define PF_K8_LD   80                     // LDS row pitch (bytes) of the int8 K tile
-#define PF_KH_LD   144                    // LDS row pitch (bytes) of the fp16 K tile
-#define PF_V_LD    144                    // LDS row pitch (bytes) of the fp16 V tile
 #define PF_Q_LD    144                    // LDS row pitch (bytes) of the fp16 Q block
 
+// Tile modes: which query blocks score in int8.  Exactness is decided per
+// (32-query tile, 64-key tile) and can only be lost as the query index grows,
+// so a 64-query block is all-int8, mixed (queries 0-31 exact, 32-63 int8) or
+// all-exact.
+enum { PF_INT8 = 0, PF_MIXED = 1, PF_EXACT = 2 };
+
+// One LDS stage of a 64-key tile.  The tiles are filled by LDS DMA (64 lanes
+// x 16 contiguous bytes per instruction, no padding possible), so bank
+// conflicts are avoided by XOR-swizzling the 16-byte chunk index with row
+// bits chosen for each array's read pattern:
+//   k8 (64 B rows, 16 rows x one chunk per read)     chunk c at c ^ ((r>>2)&3)
+//   kh (128 B rows, 16 rows x one chunk per read)    chunk c at c ^ ((r>>1)&7)
+//   v  (128 B rows, transposed reads: 4 rows x 32 B) chunk c at c ^ (((r>>1)&3)<<1)
 struct alignas(16) PfStage {
-    int8_t   k8[PF_BK * PF_K8_LD];        // [key][64 B + pad]
-    int8_t   kh[PF_BK * PF_KH_LD];        // [key][64 fp16 + pad]
-    int8_t   v[PF_BK * PF_V_LD];          // [key][64 fp16 + pad], row-major
-    float    ks[PF_BK];                   // int8 K scales of the tile
+    int8_t k8[PF_BK * 64];                // int8 K [key][64]
+    float  ks[PF_BK];                     // int8 K scales
+    int8_t kh[PF_BK * 128];               // fp16 K [key][64] (exact tiles)
+    int8_t v[PF_BK * 128];                // fp16 V [key][64]
 };
+__device__ __forceinline__ int pf_sw_k8(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int pf_sw_kh(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int pf_sw_v(int r)  { return ((r >> 1) & 3) << 1; }
 
 // Exact-tile predicate of the reference (prefill.cu:1380-1382), stated on its
 // 64-key tiles: tile kt64 is exact for the 32-query tile qt32 iff
@@ -135,8 +148,11 @@ __device__ __forceinline__ lk_i4 lk_mfma_qk8(lk_i4 kfrag, lk_i4 qfrag) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(kfrag, qfrag, z, 0, 0, 0);
 }
 
+#ifndef PF_WG_PER_CU
+#define PF_WG_PER_CU 2
+#endif
 template <bool INT8>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, PF_WG_PER_CU)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
              const float * __restrict__ qcs, const _Float16 * __restrict__ qh, int m, int P,
              const int8_t * __restrict__ k8, const float * __restrict__ ksc, int kstride,
@@ -152,14 +168,15 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     const int kvh  = blockIdx.y;
     const int qt   = (kvh < LK_N_KV_HEADS / 2) ? (int) (gridDim.x - 1 - blockIdx.x) : (int) blockIdx.x;
     const int tid  = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6;
+    const int lane = tid & 63;
+    const int w    = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col  = lane & 15, g = lane >> 4;
     const int head = kvh * LK_G + w;
     const int qbase = qt * PF_BQ;
     const int qlast = (qbase + PF_BQ < m) ? (qbase + PF_BQ) : m;
-    const int kend = P + qlast;
+    const int kend = P + qlast;                       // keys [0, kend) are visible to some row
     const int nkt = (kend + PF_BK - 1) / PF_BK;
-    const int qt32_lo = qbase / 32, qt32_hi = qbase / 32 + 1;   // qb 0-1, qb 2-3
+    const int qt32_lo = qbase / 32, qt32_hi = qbase / 32 + 1;
 
     // ---- this wave's fp16 Q block (64 rows x 128 B) into LDS, for exact tiles --
     {
@@ -174,7 +191,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     }
     // ---- int8 Q operands and per-query scalars (lane column = query) ----------
     lk_i4 qf8[PF_QB];
-    float sq[PF_QB], isq[PF_QB], qc[PF_QB];
+    float sq_[PF_QB], isq_[PF_QB], qc_[PF_QB];
 #pragma unroll
     for (int qb = 0; qb < PF_QB; ++qb) {
         const int qr = qbase + 16 * qb + col;
@@ -186,47 +203,55 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             // scores are kept in units of 1/sq until the exponent (sq > 0 scales
             // commute with the max); an all-zero query row has sq = 0 and zero
             // int8 scores, so unit scaling is exact for it
-            sq[qb] = (d > 0.0f) ? d : 1.0f;
-            isq[qb] = 1.0f / sq[qb];
-            qc[qb] = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            sq_[qb] = (d > 0.0f) ? d : 1.0f;
+            isq_[qb] = 1.0f / sq_[qb];
+            qc_[qb] = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
         } else {
-            qf8[qb] = zi; sq[qb] = 1.0f; isq[qb] = 1.0f; qc[qb] = 0.0f;
+            qf8[qb] = zi; sq_[qb] = 1.0f; isq_[qb] = 1.0f; qc_[qb] = 0.0f;
         }
     }
 
-    // ---- tile staging: global -> registers -> LDS ------------------------------
-    // K8: threads 0..127 -> key t/4, 16-byte chunk t%4; threads 128..135 the
-    // 32 scales.  Kh and V: every thread one 16-byte chunk, key t/8, chunk t%8.
-    lk_i4 rk8, rkh, rv;
-    const float * ks_h = INT8 ? ksc + (size_t) kvh * kstride : nullptr;
-    auto tile_exact = [&](int kt, int qt32) {
-        return !INT8 || lk_pf_exact(P, qt32, (kt * PF_BK) / 64, near, sink);
+    auto mode_of = [&](int kt) -> int {
+        if (!INT8) return PF_EXACT;
+        if (lk_pf_exact(P, qt32_hi, kt, near, sink)) return PF_EXACT;
+        return lk_pf_exact(P, qt32_lo, kt, near, sink) ? PF_MIXED : PF_INT8;
     };
-    auto load_regs = [&](int kt) {
-        const int kb0 = kt * PF_BK;
-        const lk_i4 zi = { 0, 0, 0, 0 };
-        if (INT8 && !tile_exact(kt, qt32_hi)) {
-            if (tid < 128) {
-                const int kpos = kb0 + (tid >> 2);
-                rk8 = (kpos < kend) ? *(const lk_i4 *) (k8 + ((size_t) kpos * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 16 * (tid & 3)) : zi;
-            } else if (tid < 136) {
-                const int sp = kb0 + 4 * (tid - 128);
-                rk8 = (sp < kend) ? *(const lk_i4 *) (ks_h + sp) : zi;
+    // a tile needs the causal mask iff its last key lies past the first query
+    auto mask_of = [&](int kt) -> bool { return kt * PF_BK + PF_BK - 1 > P + qbase; };
+
+    // ---- LDS DMA of tile kt: wave w fetches keys 16w .. 16w+15 ----------------
+    // Keys past kend are clamped to kend-1 (valid memory, finite values); they
+    // lie in masked tiles, so their p is exactly 0.
+    const uint32_t lds_st = lk_lds_addr(&st[0]);
+    const float * ks_h = INT8 ? ksc + (size_t) kvh * kstride : nullptr;
+    const int ks_clamp = ((kend - 1) / 4) * 4;        // last 16-byte chunk holding a visible key
+    auto issue = [&](int kt) {
+        const int md = mode_of(kt);
+        const uint32_t sb = lds_st + (uint32_t) ((kt & 1) * sizeof(PfStage));
+        const int kb0 = kt * PF_BK, last = kend - 1;
+        if (md != PF_EXACT) {
+            const int r = 16 * w + (lane >> 2);
+            const int c = (lane & 3) ^ pf_sw_k8(r);
+            const int kp = (kb0 + r < last) ? kb0 + r : last;
+            lk_dma16c(k8 + ((size_t) kp * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 16 * c,
+                      sb + (uint32_t) (offsetof(PfStage, k8) + 1024 * w));
+            if (lane < 4) {
+                const int s0 = kb0 + 16 * w + 4 * lane;
+                lk_dma16c(ks_h + (s0 < ks_clamp ? s0 : ks_clamp),
+                          sb + (uint32_t) (offsetof(PfStage, ks) + 64 * w));
             }
         }
-        const int kpos = kb0 + (tid >> 3);
-        const size_t goff = ((size_t) kpos * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 8 * (tid & 7);
-        if (tile_exact(kt, qt32_lo))
-            rkh = (kpos < kend) ? *(const lk_i4 *) (kc + goff) : zi;
-        rv = (kpos < kend) ? *(const lk_i4 *) (vc + goff) : zi;
-    };
-    auto store_lds = [&](int kt, PfStage & S) {
-        if (INT8 && !tile_exact(kt, qt32_hi)) {
-            if (tid < 128) *(lk_i4 *) (S.k8 + (tid >> 2) * PF_K8_LD + 16 * (tid & 3)) = rk8;
-            else if (tid < 136) *(lk_i4 *) (S.ks + 4 * (tid - 128)) = rk8;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int r = 16 * w + 8 * j + (lane >> 3);
+            const int kp = (kb0 + r < last) ? kb0 + r : last;
+            const size_t row = ((size_t) kp * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM;
+            if (md != PF_INT8)
+                lk_dma16c(kc + row + 8 * ((lane & 7) ^ pf_sw_kh(r)),
+                          sb + (uint32_t) (offsetof(PfStage, kh) + 1024 * (2 * w + j)));
+            lk_dma16c(vc + row + 8 * ((lane & 7) ^ pf_sw_v(r)),
+                      sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * w + j)));
         }
-        if (tile_exact(kt, qt32_lo)) *(lk_i4 *) (S.kh + (tid >> 3) * PF_KH_LD + 16 * (tid & 7)) = rkh;
-        *(lk_i4 *) (S.v + (tid >> 3) * PF_V_LD + 16 * (tid & 7)) = rv;
     };
 
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
@@ -247,126 +272,162 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // inside fp16 range and loses no relative precision.
     constexpr float PF_HEADROOM = 8.0f;
 
-    load_regs(0);
-    store_lds(0, st[0]);
-    __syncthreads();
+    // ---- per-lane LDS read offsets: the swizzles above depend only on the lane
+    // here, so every read below is one of these bases plus a constant.
+    const int o_k8_ = col * 64 + 16 * (g ^ (col >> 2));               // + 1024*kb
+    const int o_kh0_ = col * 128 + 16 * (g ^ (col >> 1));             // + 2048*kb
+    const int o_kh1_ = col * 128 + 16 * ((4 + g) ^ (col >> 1));       // + 2048*kb
+    const int vsw = (2 * g + ((col >> 2) >> 1)) & 3;                 // pf_sw_v(row) / 2
+    const int o_v = (4 * g + (col >> 2)) * 128 + 8 * (col & 1);      // + 4096*kk (+2048 hi)
+    int o_vd_[4];                                                    // chunk of dims 16db + 4(col&3)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o_vd_[db] = o_v + 32 * (db ^ vsw) + 16 * ((col & 3) >> 1);
+    const int o_q_ = col * PF_Q_LD + 16 * g;                          // + 16*PF_Q_LD*qb
 
-    for (int kt = 0; kt < nkt; ++kt) {
-        if (kt + 1 < nkt) load_regs(kt + 1);
-        const PfStage & S = st[kt & 1];
+    // ---- one 64-key tile.  Mode and mask are wave-uniform run-time branches:
+    // bodies specialised per mode (one loop each, or one loop with a branch to
+    // each) measured 40% slower, the register allocator then spilled.
+    auto tile = [&](const PfStage & S, int kt) {
+        const int md = mode_of(kt);
+        const bool msk = mask_of(kt);
         const int kb0 = kt * PF_BK;
-        const bool ex_lo = tile_exact(kt, qt32_lo);
-        const bool ex_hi = tile_exact(kt, qt32_hi);
-
-        // ---- scores S^T[kb][qb] (keys kb0+16kb+4g+r, query 16qb+col), x-units ----
-        float x[2][PF_QB][4];
-        if (ex_lo) {
-            lk_h8 ka[2][2];
+        // Opaque copies of the loop-invariant lane values: without them the
+        // compiler hoists every derived address and constant of all the tile
+        // loops out of the segment loop, where they all stay live and spill.
+        int o_k8 = o_k8_, o_kh0 = o_kh0_, o_kh1 = o_kh1_, o_q = o_q_, o_vd[4];
+        lk_launder(o_k8); lk_launder(o_kh0); lk_launder(o_kh1); lk_launder(o_q);
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
+        for (int i = 0; i < 4; ++i) { o_vd[i] = o_vd_[i]; lk_launder(o_vd[i]); }
+        float sq[PF_QB], isq[PF_QB], qc[PF_QB];
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    ka[kb][ks] = *(const lk_h8 *) (S.kh + (16 * kb + col) * PF_KH_LD + 64 * ks + 16 * g);
+        for (int i = 0; i < PF_QB; ++i) {
+            sq[i] = sq_[i]; isq[i] = isq_[i]; qc[i] = qc_[i];
+            lk_launder(sq[i]); lk_launder(isq[i]); lk_launder(qc[i]);
+        }
+        lk_i4 ka[4];                        // int8 K fragments (key row 16kb+col)
+        lk_f4 sk[4];                        // their scales (keys 16kb+4g+i)
+        if (md != PF_EXACT) {
 #pragma unroll
-            for (int qb = 0; qb < PF_QB; ++qb) {
-                const bool ex = (qb < 2) ? ex_lo : ex_hi;
-                if (!ex) continue;
-                const int8_t * qrow = s_q[w] + (16 * qb + col) * PF_Q_LD + 16 * g;
-                const lk_h8 qf0 = *(const lk_h8 *) qrow;
-                const lk_h8 qf1 = *(const lk_h8 *) (qrow + 64);
+            for (int kb = 0; kb < 4; ++kb) {
+                ka[kb] = *(const lk_i4 *) (S.k8 + o_k8 + 1024 * kb);
+                sk[kb] = *(const lk_f4 *) (S.ks + 16 * kb + 4 * g);
+            }
+        }
+        lk_h8 pb[PF_QB][2];
+        // Two query blocks at a time (scores of 64 keys x 32 queries in flight);
+        // in a mixed tile the first pair is exact, the second int8.
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    lk_f4 c = { 0.f, 0.f, 0.f, 0.f };
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kb][0], qf0, c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kb][1], qf1, c, 0, 0, 0);
+        for (int hq = 0; hq < 2; ++hq) {
+            const bool ex = (md == PF_EXACT) || (md == PF_MIXED && hq == 0);
+            float x[4][2][4];               // [key block][query block 2hq+j][i]: key kb0+16kb+4g+i
+            if (ex) {
+                lk_h8 qa[2][2];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        x[kb][qb][r] = INT8 ? fmaf(c[r], LK_LOG2E_F, -qc[qb]) * isq[qb] : c[r] * LK_LOG2E_F;
+                for (int j = 0; j < 2; ++j) {
+                    const int8_t * qrow = s_q[w] + o_q + 16 * PF_Q_LD * (2 * hq + j);
+                    qa[j][0] = *(const lk_h8 *) qrow;
+                    qa[j][1] = *(const lk_h8 *) (qrow + 64);
+                }
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    const lk_h8 k0 = *(const lk_h8 *) (S.kh + o_kh0 + 2048 * kb);
+                    const lk_h8 k1 = *(const lk_h8 *) (S.kh + o_kh1 + 2048 * kb);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int qb = 2 * hq + j;
+                        lk_f4 c = { 0.f, 0.f, 0.f, 0.f };
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qa[j][0], c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qa[j][1], c, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            x[kb][j][i] = INT8 ? fmaf(c[i], LK_LOG2E_F, -qc[qb]) * isq[qb] : c[i] * LK_LOG2E_F;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const lk_i4 c = lk_mfma_qk8(ka[kb], qf8[2 * hq + j]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) x[kb][j][i] = (float) c[i] * sk[kb][i];
+                    }
+            }
+            if (msk) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    // key kb0+16kb+4g+i is masked iff 16kb+i > qpos - kb0 - 4g
+                    const int dq = P + qbase + 16 * (2 * hq + j) + col - kb0 - 4 * g;
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (16 * kb + i > dq) x[kb][j][i] = -INFINITY;
                 }
             }
-        }
-        if (INT8 && !ex_hi) {
-            lk_i4 ka8[2];
-            float4 skv[2];
+            // ---- online softmax, per query (lane column); exponent = sq*(x - m) --
+            float mx[2];
+            bool need[2];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                ka8[kb] = *(const lk_i4 *) (S.k8 + (16 * kb + col) * PF_K8_LD + 16 * g);
-                skv[kb] = *(const float4 *) (S.ks + 16 * kb + 4 * g);
+            for (int j = 0; j < 2; ++j) {
+                const int qb = 2 * hq + j;
+                float v = x[0][j][0];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v = fmaxf(v, x[kb][j][i]);
+                mx[j] = lk_xrow_max(v);                        // the 4 lane groups of this query
+                // key 0 is visible to every query, so mrun is finite after tile 0
+                need[j] = mx[j] > mrun[qb] + PF_HEADROOM * isq[qb];
             }
+            if (__ballot(need[0] || need[1])) {                // wave-uniform branch
 #pragma unroll
-            for (int qb = 0; qb < PF_QB; ++qb) {
-                const bool ex = (qb < 2) ? ex_lo : ex_hi;
-                if (ex) continue;
+                for (int j = 0; j < 2; ++j) {
+                    const int qb = 2 * hq + j;
+                    const float alpha = need[j] ? lk_exp2((mrun[qb] - mx[j]) * sq[qb]) : 1.0f;
+                    mrun[qb] = need[j] ? mx[j] : mrun[qb];
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    const lk_i4 c = lk_mfma_qk8(ka8[kb], qf8[qb]);
-                    x[kb][qb][0] = (float) c[0] * skv[kb].x;
-                    x[kb][qb][1] = (float) c[1] * skv[kb].y;
-                    x[kb][qb][2] = (float) c[2] * skv[kb].z;
-                    x[kb][qb][3] = (float) c[3] * skv[kb].w;
+                    for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
                 }
             }
-        }
-
-        // ---- causal mask (only tiles that reach past the block's first query) ---
-        if (kb0 + PF_BK - 1 > P + qbase) {
 #pragma unroll
-            for (int qb = 0; qb < PF_QB; ++qb) {
-                const int qpos = P + qbase + 16 * qb + col;
+            for (int j = 0; j < 2; ++j) {
+                const int qb = 2 * hq + j;
+                const float msq = mrun[qb] * sq[qb];
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (kb0 + 16 * kb + 4 * g + r > qpos) x[kb][qb][r] = -INFINITY;
+                    for (int i = 0; i < 4; ++i) {
+                        pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -msq));
+                        pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -msq));
+                    }
             }
         }
-
-        // ---- online softmax, per query (lane column); exponent = sq * (x - m) ---
+        // ---- O^T += V^T . P^T over the 64 keys, 32 per MFMA -----------------------
 #pragma unroll
-        for (int qb = 0; qb < PF_QB; ++qb) {
-            float mx = fmaxf(fmaxf(fmaxf(x[0][qb][0], x[0][qb][1]), fmaxf(x[0][qb][2], x[0][qb][3])),
-                             fmaxf(fmaxf(x[1][qb][0], x[1][qb][1]), fmaxf(x[1][qb][2], x[1][qb][3])));
-            mx = lk_xrow_max(mx);
-            // key 0 is visible to every query, so mrun is finite after tile 0
-            const bool need = mx > mrun[qb] + PF_HEADROOM * isq[qb];
-            if (__ballot(need)) {                              // wave-uniform branch
-                const float alpha = need ? lk_exp2((mrun[qb] - mx) * sq[qb]) : 1.0f;
-                mrun[qb] = need ? mx : mrun[qb];
+        for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-                for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
+            for (int db = 0; db < 4; ++db) {
+                const lk_h4 lo = lk_ds_tr4(S.v + o_vd[db] + 4096 * kk);          // keys 32kk + 4g + col/4
+                const lk_h4 hi = lk_ds_tr4(S.v + o_vd[db] + 4096 * kk + 2048);   // keys +16
+                const lk_h8 va = { lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3] };
+#pragma unroll
+                for (int qb = 0; qb < PF_QB; ++qb)
+                    acc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qb][kk], acc[db][qb], 0, 0, 0);
             }
-            const float msq = mrun[qb] * sq[qb];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) x[kb][qb][r] = lk_exp2(fmaf(x[kb][qb][r], sq[qb], -msq));
-        }
-
-        // ---- O^T += V^T . P^T over the 32 keys -----------------------------------
-        lk_h8 pb[PF_QB];
-#pragma unroll
-        for (int qb = 0; qb < PF_QB; ++qb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                pb[qb][r]     = (_Float16) x[0][qb][r];
-                pb[qb][4 + r] = (_Float16) x[1][qb][r];
-            }
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const int8_t * vp = S.v + (col >> 2) * PF_V_LD + 2 * (16 * db + 4 * (col & 3));
-            const lk_h4 lo = lk_ds_tr4(vp + (4 * g) * PF_V_LD);
-            const lk_h4 hi = lk_ds_tr4(vp + (16 + 4 * g) * PF_V_LD);
-            const lk_h8 va = { lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3] };
 #pragma unroll
             for (int qb = 0; qb < PF_QB; ++qb)
-                acc[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qb], acc[db][qb], 0, 0, 0);
+                acc[4][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[qb][kk], acc[4][qb], 0, 0, 0);
         }
-#pragma unroll
-        for (int qb = 0; qb < PF_QB; ++qb)
-            acc[4][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[qb], acc[4][qb], 0, 0, 0);
+    };
 
-        if (kt + 1 < nkt) store_lds(kt + 1, st[(kt + 1) & 1]);
-        __syncthreads();
+    // ---- tile loop: one barrier per tile; tile kt+1 streams in while kt computes
+    issue(0);
+    for (int kt = 0; kt < nkt; ++kt) {
+        lk_wait_vm<0>();                                  // this wave's part of tile kt landed
+        __syncthreads();                                  // ... everyone's; tile kt-1 fully consumed
+        if (kt + 1 < nkt) issue(kt + 1);                  // into the stage tile kt-1 used
+        tile(st[kt & 1], kt);
     }
 
     // ---- epilogue: l over the 4 lane groups, then o[q][head*64 + d] -------------
