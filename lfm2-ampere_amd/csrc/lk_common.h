@@ -35,6 +35,8 @@
 #endif
 
 // ---- vector types ---------------------------------------------------------------
+typedef unsigned short lk_u16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned short lk_u16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 lk_h8  __attribute__((ext_vector_type(8)));
 typedef _Float16 lk_h4  __attribute__((ext_vector_type(4)));
 typedef float    lk_f4  __attribute__((ext_vector_type(4)));
@@ -154,6 +156,12 @@ __device__ __forceinline__ void lk_dma16(const void * src, uint32_t lds) {
 __device__ __forceinline__ void lk_dma16c(const void * src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                  :: "v"(src), "s"(lds) : "memory", "m0");
+}
+// The same with a wave-uniform 64-bit base (SGPRs) plus a per-lane 32-bit
+// byte offset: moving the source costs only scalar adds.
+__device__ __forceinline__ void lk_dma16c_so(const void * sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding).

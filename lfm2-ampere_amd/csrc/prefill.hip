@@ -220,15 +220,45 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     auto mask_of = [&](int kt) -> bool { return kt * PF_BK + PF_BK - 1 > P + qbase; };
 
     // ---- LDS DMA of tile kt: wave w fetches keys 16w .. 16w+15 ----------------
-    // Keys past kend are clamped to kend-1 (valid memory, finite values); they
-    // lie in masked tiles, so their p is exactly 0.
     const uint32_t lds_st = lk_lds_addr(&st[0]);
     const float * ks_h = INT8 ? ksc + (size_t) kvh * kstride : nullptr;
     const int ks_clamp = ((kend - 1) / 4) * 4;        // last 16-byte chunk holding a visible key
+    // Per-lane byte offsets of the DMA sources relative to the tile's first key
+    // (the kv head folded in); the tile base itself is wave-uniform.
+    const int r_k8 = 16 * w + (lane >> 2);
+    const uint32_t so_k8 = (uint32_t) ((r_k8 * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 16 * ((lane & 3) ^ pf_sw_k8(r_k8)));
+    const uint32_t so_ks = (uint32_t) (4 * (16 * w + 4 * lane));
+    uint32_t so_kh[2], so_v[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = 16 * w + 8 * j + (lane >> 3);
+        const uint32_t row = (uint32_t) ((r * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM * 2);
+        so_kh[j] = row + 16 * ((lane & 7) ^ pf_sw_kh(r));
+        so_v[j]  = row + 16 * ((lane & 7) ^ pf_sw_v(r));
+    }
     auto issue = [&](int kt) {
         const int md = mode_of(kt);
         const uint32_t sb = lds_st + (uint32_t) ((kt & 1) * sizeof(PfStage));
-        const int kb0 = kt * PF_BK, last = kend - 1;
+        const int kb0 = kt * PF_BK;
+        if (kb0 + PF_BK <= kend) {                        // whole tile visible: no clamping
+            const int8_t * kb8 = k8 + (size_t) kb0 * LK_KV_ROW;
+            const _Float16 * kbh = kc + (size_t) kb0 * LK_KV_ROW;
+            const _Float16 * kbv = vc + (size_t) kb0 * LK_KV_ROW;
+            if (md != PF_EXACT) {
+                lk_dma16c_so(kb8, so_k8, sb + (uint32_t) (offsetof(PfStage, k8) + 1024 * w));
+                if (lane < 4) lk_dma16c_so(ks_h + kb0, so_ks, sb + (uint32_t) (offsetof(PfStage, ks) + 64 * w));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (md != PF_INT8)
+                    lk_dma16c_so(kbh, so_kh[j], sb + (uint32_t) (offsetof(PfStage, kh) + 1024 * (2 * w + j)));
+                lk_dma16c_so(kbv, so_v[j], sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * w + j)));
+            }
+            return;
+        }
+        // the block's last tile: keys past kend are clamped to kend-1 (valid
+        // memory, finite values); they are masked, so their p is exactly 0
+        const int last = kend - 1;
         if (md != PF_EXACT) {
             const int r = 16 * w + (lane >> 2);
             const int c = (lane & 3) ^ pf_sw_k8(r);
@@ -271,6 +301,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // 2^PF_HEADROOM in p (so most tiles skip the rescale); p <= 2^8 stays far
     // inside fp16 range and loses no relative precision.
     constexpr float PF_HEADROOM = 8.0f;
+    constexpr unsigned PF_P_LIMIT_BITS = 0x5C00u;          // fp16 bits of 2^PF_HEADROOM = 256
 
     // ---- per-lane LDS read offsets: the swizzles above depend only on the lane
     // here, so every read below is one of these bases plus a constant.
@@ -366,41 +397,55 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 }
             }
             // ---- online softmax, per query (lane column); exponent = sq*(x - m) --
-            float mx[2];
-            bool need[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int qb = 2 * hq + j;
-                float v = x[0][j][0];
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) v = fmaxf(v, x[kb][j][i]);
-                mx[j] = lk_xrow_max(v);                        // the 4 lane groups of this query
-                // key 0 is visible to every query, so mrun is finite after tile 0
-                need[j] = mx[j] > mrun[qb] + PF_HEADROOM * isq[qb];
-            }
-            if (__ballot(need[0] || need[1])) {                // wave-uniform branch
+            // p is formed against the running max first.  The exact tile max is
+            // only needed when some p would exceed 2^PF_HEADROOM (or the max is
+            // still -inf: first tile): that is detected on the fp16 bit patterns
+            // of p (p >= 0, so their u16 order is the f16 order, and inf/NaN
+            // sort above 2^8), two per lane op, with no cross-lane reduction.
+            auto make_p = [&]() {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int qb = 2 * hq + j;
-                    const float alpha = need[j] ? lk_exp2((mrun[qb] - mx[j]) * sq[qb]) : 1.0f;
-                    mrun[qb] = need[j] ? mx[j] : mrun[qb];
+                    const float msq = mrun[qb] * sq[qb];
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -msq));
+                            pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -msq));
+                        }
+                }
+            };
+            make_p();
+            lk_u16x2 pm = { 0, 0 };
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const lk_u16x8 u = __builtin_bit_cast(lk_u16x8, pb[2 * hq + j][kk]);
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2)
+                        pm = __builtin_elementwise_max(pm, (lk_u16x2){ u[e], u[e + 1] });
+                }
+            const unsigned pmax = (pm[0] > pm[1]) ? pm[0] : pm[1];
+            if (__ballot(pmax > PF_P_LIMIT_BITS)) {            // wave-uniform, rare
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int qb = 2 * hq + j;
+                    float v = x[0][j][0];
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) v = fmaxf(v, x[kb][j][i]);
+                    const float mx = lk_xrow_max(v);           // the 4 lane groups of this query
+                    // key 0 is visible to every query, so mrun is finite after tile 0
+                    const bool need = mx > mrun[qb] + PF_HEADROOM * isq[qb];
+                    const float alpha = need ? lk_exp2((mrun[qb] - mx) * sq[qb]) : 1.0f;
+                    mrun[qb] = need ? mx : mrun[qb];
 #pragma unroll
                     for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
                 }
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int qb = 2 * hq + j;
-                const float msq = mrun[qb] * sq[qb];
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -msq));
-                        pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -msq));
-                    }
+                make_p();
             }
         }
         // ---- O^T += V^T . P^T over the 64 keys, 32 per MFMA -----------------------
