@@ -130,11 +130,6 @@ __host__ __device__ __forceinline__ void lk_attn_slices(int seq, int & ns, int &
     chunk = (seq + s - 1) / s;
 }
 
-// Makes a register value opaque to the optimiser (no code is emitted), so
-// values derived from it are not hoisted out of the enclosing loop.
-template <typename T>
-__device__ __forceinline__ void lk_launder(T & v) { asm volatile("" : "+v"(v)); }
-
 // ---- LDS DMA (global_load_lds_dwordx4) --------------------------------------
 // Byte address of an LDS object (the value M0 takes for an LDS DMA).
 __device__ __forceinline__ uint32_t lk_lds_addr(const void * p) {

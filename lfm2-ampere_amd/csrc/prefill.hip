@@ -148,11 +148,8 @@ __device__ __forceinline__ lk_i4 lk_mfma_qk8(lk_i4 kfrag, lk_i4 qfrag) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(kfrag, qfrag, z, 0, 0, 0);
 }
 
-#ifndef PF_WG_PER_CU
-#define PF_WG_PER_CU 2
-#endif
 template <bool INT8>
-__global__ void __launch_bounds__(256, PF_WG_PER_CU)
+__global__ void __launch_bounds__(256, 2)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
              const float * __restrict__ qcs, const _Float16 * __restrict__ qh, int m, int P,
              const int8_t * __restrict__ k8, const float * __restrict__ ksc, int kstride,
@@ -191,7 +188,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     }
     // ---- int8 Q operands and per-query scalars (lane column = query) ----------
     lk_i4 qf8[PF_QB];
-    float sq_[PF_QB], isq_[PF_QB], qc_[PF_QB];
+    float sq[PF_QB], isq[PF_QB], qc[PF_QB];
 #pragma unroll
     for (int qb = 0; qb < PF_QB; ++qb) {
         const int qr = qbase + 16 * qb + col;
@@ -203,11 +200,11 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             // scores are kept in units of 1/sq until the exponent (sq > 0 scales
             // commute with the max); an all-zero query row has sq = 0 and zero
             // int8 scores, so unit scaling is exact for it
-            sq_[qb] = (d > 0.0f) ? d : 1.0f;
-            isq_[qb] = 1.0f / sq_[qb];
-            qc_[qb] = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            sq[qb] = (d > 0.0f) ? d : 1.0f;
+            isq[qb] = 1.0f / sq[qb];
+            qc[qb] = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
         } else {
-            qf8[qb] = zi; sq_[qb] = 1.0f; isq_[qb] = 1.0f; qc_[qb] = 0.0f;
+            qf8[qb] = zi; sq[qb] = 1.0f; isq[qb] = 1.0f; qc[qb] = 0.0f;
         }
     }
 
@@ -305,15 +302,15 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 
     // ---- per-lane LDS read offsets: the swizzles above depend only on the lane
     // here, so every read below is one of these bases plus a constant.
-    const int o_k8_ = col * 64 + 16 * (g ^ (col >> 2));               // + 1024*kb
-    const int o_kh0_ = col * 128 + 16 * (g ^ (col >> 1));             // + 2048*kb
-    const int o_kh1_ = col * 128 + 16 * ((4 + g) ^ (col >> 1));       // + 2048*kb
+    const int o_k8 = col * 64 + 16 * (g ^ (col >> 2));               // + 1024*kb
+    const int o_kh0 = col * 128 + 16 * (g ^ (col >> 1));             // + 2048*kb
+    const int o_kh1 = col * 128 + 16 * ((4 + g) ^ (col >> 1));       // + 2048*kb
     const int vsw = (2 * g + ((col >> 2) >> 1)) & 3;                 // pf_sw_v(row) / 2
     const int o_v = (4 * g + (col >> 2)) * 128 + 8 * (col & 1);      // + 4096*kk (+2048 hi)
-    int o_vd_[4];                                                    // chunk of dims 16db + 4(col&3)
+    int o_vd[4];                                                    // chunk of dims 16db + 4(col&3)
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o_vd_[db] = o_v + 32 * (db ^ vsw) + 16 * ((col & 3) >> 1);
-    const int o_q_ = col * PF_Q_LD + 16 * g;                          // + 16*PF_Q_LD*qb
+    for (int db = 0; db < 4; ++db) o_vd[db] = o_v + 32 * (db ^ vsw) + 16 * ((col & 3) >> 1);
+    const int o_q = col * PF_Q_LD + 16 * g;                          // + 16*PF_Q_LD*qb
 
     // ---- one 64-key tile.  Mode and mask are wave-uniform run-time branches:
     // bodies specialised per mode (one loop each, or one loop with a branch to
@@ -322,19 +319,6 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         const int md = mode_of(kt);
         const bool msk = mask_of(kt);
         const int kb0 = kt * PF_BK;
-        // Opaque copies of the loop-invariant lane values: without them the
-        // compiler hoists every derived address and constant of all the tile
-        // loops out of the segment loop, where they all stay live and spill.
-        int o_k8 = o_k8_, o_kh0 = o_kh0_, o_kh1 = o_kh1_, o_q = o_q_, o_vd[4];
-        lk_launder(o_k8); lk_launder(o_kh0); lk_launder(o_kh1); lk_launder(o_q);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { o_vd[i] = o_vd_[i]; lk_launder(o_vd[i]); }
-        float sq[PF_QB], isq[PF_QB], qc[PF_QB];
-#pragma unroll
-        for (int i = 0; i < PF_QB; ++i) {
-            sq[i] = sq_[i]; isq[i] = isq_[i]; qc[i] = qc_[i];
-            lk_launder(sq[i]); lk_launder(isq[i]); lk_launder(qc[i]);
-        }
         lk_i4 ka[4];                        // int8 K fragments (key row 16kb+col)
         lk_f4 sk[4];                        // their scales (keys 16kb+4g+i)
         if (md != PF_EXACT) {
