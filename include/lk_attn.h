@@ -152,6 +152,16 @@ int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * qcs,
 int lk_pf_attn(const void * qh, int m, int P, const void * kc, const void * vc,
                float * o, void * stream);
 
+/* Both attention entry points balance causal chunks by splitting the key range
+ * of long query blocks across workgroups (merged by a second kernel, in a fixed
+ * order: output stays run-to-run bit-identical).  The split uses a static
+ * 64 MiB device scratch of the library; calls on one device that overlap in
+ * time (different streams) must not both split.  Process-wide knob, for tests
+ * and tuning: -1 never split, 0 automatic (default), n > 0 parts of at most n
+ * key tiles of 64.  No counterpart in the reference (its kernels do not
+ * split). */
+int lk_pf_split_override(int tiles);
+
 /* ---- test hook --------------------------------------------------------------
  * The raw int32 Q.K^T sums of the int8 scoring path, computed by the same
  * matrix-core routine lk_pf_attn8 uses:  s[head][i][j] = sum_d q8[i][head][d] *

@@ -28,6 +28,7 @@
 //     P.V (as the reference does), accumulation in fp32 throughout.
 #include "lk_common.h"
 #include <math.h>
+#include <algorithm>
 
 // ---------------------------------------------------------------------------
 // int8 quantisers.  One wave per 64-wide (row, head), one value per lane.
@@ -148,22 +149,101 @@ __device__ __forceinline__ lk_i4 lk_mfma_qk8(lk_i4 kfrag, lk_i4 qfrag) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(kfrag, qfrag, z, 0, 0, 0);
 }
 
+// ---- split-K work items (load balance of causal chunks) -----------------------
+// Query block qt of a chunk sees key tiles [0, nkt(qt)); with P = 0 that grows
+// from 1 to m/64 tiles, and a CU holding a long and a short block runs the
+// long one's tail at one wave per SIMD (about half speed).  With lsplit > 0,
+// blocks longer than lsplit tiles are cut into np near-equal key ranges
+// ("parts"), every part writes an unnormalised partial (m, l, acc) and
+// lk_k_pf_combine merges them in part order.  Items are enumerated longest
+// block first (kv head fastest), so the hardware dispatcher hands out the big
+// items first.  A part never starts after the block's first diagonal tile,
+// so every query sees at least one key in every part.
+__host__ __device__ inline int pf_nkt(int qt, int m, int P) {
+    const int qlast = (qt * PF_BQ + PF_BQ < m) ? qt * PF_BQ + PF_BQ : m;
+    return (P + qlast + PF_BK - 1) / PF_BK;
+}
+__host__ __device__ inline void pf_parts(int qt, int m, int P, int lsplit, int & np, int & per) {
+    const int nkt = pf_nkt(qt, m, P);
+    np = (lsplit > 0) ? (nkt + lsplit - 1) / lsplit : 1;
+    if (np < 1) np = 1;
+    per = (nkt + np - 1) / np;
+    const int kdiag = (P + qt * PF_BQ) / PF_BK;        // tile holding the block's first query
+    while (np > 1 && (np - 1) * per > kdiag) { --np; per = (nkt + np - 1) / np; }
+}
+// The launch's work list, built on the host and passed by value: items sorted
+// longest first (kv head fastest in the grid), each = (block, part); slot0[q]
+// is the first partial slot of split block q; split_qt lists the split blocks.
+#define PF_MAX_ITEMS 640
+#define PF_MAX_QB    128
+struct PfWork {
+    int n_items, n_split, lsplit;                      // n_items 0: unsplit launch
+    uint16_t item[PF_MAX_ITEMS];                        // qt | part << 8
+    int16_t slot0[PF_MAX_QB];
+    uint8_t split_qt[PF_MAX_QB];
+};
+// Partials of a part, per (slot, kv head): acc as [head][16 dim chunks][64
+// rows] of float4 (coalesced for the writing lanes and the merging lanes),
+// then (m, l) as [head][64 rows] of float2; m is in the log2 domain of p.
+#define PF_PART_ACC   (LK_G * 16 * PF_BQ * 4)           // floats
+#define PF_PART_SLOT  (PF_PART_ACC + LK_G * PF_BQ * 2)  // floats per (part, kv head)
+// Static scratch for the partials, 64 MiB per device.
+#define PF_PART_CAP   (16u << 20)                        // floats
+__device__ float g_pf_part[PF_PART_CAP];
+#ifdef PF_WG_TRACE
+// Measurement builds only: per-workgroup (start, end, HW_ID, XCC_ID).
+__device__ uint4 g_pf_trace[16384];
+extern "C" int lk_pf_trace_read(void * dst, int n) {
+    return (int) hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_pf_trace), (size_t) n * sizeof(uint4));
+}
+#endif
+
 template <bool INT8>
 __global__ void __launch_bounds__(256, 2)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
              const float * __restrict__ qcs, const _Float16 * __restrict__ qh, int m, int P,
              const int8_t * __restrict__ k8, const float * __restrict__ ksc, int kstride,
              const _Float16 * __restrict__ kc, const _Float16 * __restrict__ vc,
-             int near, int sink, float * __restrict__ o) {
+             int near, int sink, float * __restrict__ o, const PfWork work, float * __restrict__ pbuf) {
     __shared__ PfStage st[2];
     __shared__ __attribute__((aligned(16))) int8_t s_q[4][PF_BQ * PF_Q_LD];   // fp16 Q, per head
-    // Causal work grows with the query block.  Workgroups are dispatched in
-    // linear order and the second half of the grid lands beside the first half
-    // on the CUs, so kv heads 0-3 take the query blocks longest-first and kv
-    // heads 4-7 shortest-first: co-resident workgroups then pair a long block
-    // with a short one.
-    const int kvh  = blockIdx.y;
-    const int qt   = (kvh < LK_N_KV_HEADS / 2) ? (int) (gridDim.x - 1 - blockIdx.x) : (int) blockIdx.x;
+#ifdef PF_WG_TRACE
+    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+    auto trace_end = [&](int ntiles) {
+        if (threadIdx.x == 0) {
+            const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
+            const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+            const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);
+            const unsigned id = blockIdx.x + blockIdx.y * gridDim.x;
+            if (id < 8192) g_pf_trace[id] = make_uint4((unsigned) t_start, (unsigned) t_end, hw, (xcc & 255) | ((unsigned) ntiles << 8));
+        }
+    };
+#else
+    auto trace_end = [](int) {};
+#endif
+    // Causal work grows with the query block.  Unsplit launches: workgroups
+    // are dispatched in linear order and the second half of the grid lands
+    // beside the first half on the CUs, so kv heads 0-3 take the query blocks
+    // longest-first and kv heads 4-7 shortest-first: co-resident workgroups
+    // then pair a long block with a short one.  Split launches: one work item
+    // (block, key range) per workgroup, longest first.
+    int kvh, qt, kt_lo, kt_hi, pslot = -1;
+    if (work.n_items == 0) {
+        kvh = blockIdx.y;
+        qt  = (kvh < LK_N_KV_HEADS / 2) ? (int) (gridDim.x - 1 - blockIdx.x) : (int) blockIdx.x;
+        kt_lo = 0; kt_hi = pf_nkt(qt, m, P);
+    } else {
+        kvh = blockIdx.x % LK_N_KV_HEADS;
+        const int it = work.item[blockIdx.x / LK_N_KV_HEADS];
+        qt = it & 255;
+        const int part = it >> 8;
+        int np, per;
+        pf_parts(qt, m, P, work.lsplit, np, per);
+        kt_lo = part * per;
+        kt_hi = pf_nkt(qt, m, P);
+        if (kt_lo + per < kt_hi) kt_hi = kt_lo + per;
+        if (np > 1) pslot = work.slot0[qt] + part;
+    }
     const int tid  = threadIdx.x;
     const int lane = tid & 63;
     const int w    = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -172,41 +252,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     const int qbase = qt * PF_BQ;
     const int qlast = (qbase + PF_BQ < m) ? (qbase + PF_BQ) : m;
     const int kend = P + qlast;                       // keys [0, kend) are visible to some row
-    const int nkt = (kend + PF_BK - 1) / PF_BK;
     const int qt32_lo = qbase / 32, qt32_hi = qbase / 32 + 1;
-
-    // ---- this wave's fp16 Q block (64 rows x 128 B) into LDS, for exact tiles --
-    {
-        const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = (lane >> 3) + 8 * i, c = lane & 7;
-            const int qr = qbase + r;
-            const lk_h8 v = (qr < m) ? *(const lk_h8 *) (qh + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 8 * c) : z8;
-            *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * c) = v;
-        }
-    }
-    // ---- int8 Q operands and per-query scalars (lane column = query) ----------
-    lk_i4 qf8[PF_QB];
-    float sq[PF_QB], isq[PF_QB], qc[PF_QB];
-#pragma unroll
-    for (int qb = 0; qb < PF_QB; ++qb) {
-        const int qr = qbase + 16 * qb + col;
-        const bool ok = qr < m;
-        const lk_i4 zi = { 0, 0, 0, 0 };
-        if (INT8) {
-            qf8[qb] = ok ? *(const lk_i4 *) (q8 + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 16 * g) : zi;
-            const float d = ok ? qsc[(size_t) qr * LK_N_HEADS + head] : 0.0f;
-            // scores are kept in units of 1/sq until the exponent (sq > 0 scales
-            // commute with the max); an all-zero query row has sq = 0 and zero
-            // int8 scores, so unit scaling is exact for it
-            sq[qb] = (d > 0.0f) ? d : 1.0f;
-            isq[qb] = 1.0f / sq[qb];
-            qc[qb] = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
-        } else {
-            qf8[qb] = zi; sq[qb] = 1.0f; isq[qb] = 1.0f; qc[qb] = 0.0f;
-        }
-    }
 
     auto mode_of = [&](int kt) -> int {
         if (!INT8) return PF_EXACT;
@@ -280,6 +326,44 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                       sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * w + j)));
         }
     };
+
+    // The first tile's DMA goes out before the Q loads below, so that the two
+    // memory latencies overlap.
+    issue(kt_lo);
+
+    // ---- this wave's fp16 Q block (64 rows x 128 B) into LDS, for exact tiles --
+    {
+        const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = (lane >> 3) + 8 * i, c = lane & 7;
+            const int qr = qbase + r;
+            const lk_h8 v = (qr < m) ? *(const lk_h8 *) (qh + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 8 * c) : z8;
+            *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * c) = v;
+        }
+    }
+    // ---- int8 Q operands and per-query scalars (lane column = query) ----------
+    lk_i4 qf8[PF_QB];
+    float sq[PF_QB], isq[PF_QB], qc[PF_QB];
+#pragma unroll
+    for (int qb = 0; qb < PF_QB; ++qb) {
+        const int qr = qbase + 16 * qb + col;
+        const bool ok = qr < m;
+        const lk_i4 zi = { 0, 0, 0, 0 };
+        if (INT8) {
+            qf8[qb] = ok ? *(const lk_i4 *) (q8 + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 16 * g) : zi;
+            const float d = ok ? qsc[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            // scores are kept in units of 1/sq until the exponent (sq > 0 scales
+            // commute with the max); an all-zero query row has sq = 0 and zero
+            // int8 scores, so unit scaling is exact for it
+            sq[qb] = (d > 0.0f) ? d : 1.0f;
+            isq[qb] = 1.0f / sq[qb];
+            qc[qb] = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+        } else {
+            qf8[qb] = zi; sq[qb] = 1.0f; isq[qb] = 1.0f; qc[qb] = 0.0f;
+        }
+    }
+
 
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
     // all-ones A operand, so every lane of query column q accumulates
@@ -451,12 +535,37 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     };
 
     // ---- tile loop: one barrier per tile; tile kt+1 streams in while kt computes
-    issue(0);
-    for (int kt = 0; kt < nkt; ++kt) {
+#ifdef PF_WG_TRACE
+    uint64_t t_a = __builtin_amdgcn_s_memrealtime(), t_b = 0, t_c = 0;
+#endif
+    for (int kt = kt_lo; kt < kt_hi; ++kt) {
         lk_wait_vm<0>();                                  // this wave's part of tile kt landed
         __syncthreads();                                  // ... everyone's; tile kt-1 fully consumed
-        if (kt + 1 < nkt) issue(kt + 1);                  // into the stage tile kt-1 used
+#ifdef PF_WG_TRACE
+        if (kt == kt_lo) t_b = __builtin_amdgcn_s_memrealtime();
+        if (kt == kt_lo + 1) t_c = __builtin_amdgcn_s_memrealtime();
+#endif
+        if (kt + 1 < kt_hi) issue(kt + 1);                // into the stage tile kt-1 used
         tile(st[kt & 1], kt);
+    }
+#ifdef PF_WG_TRACE
+    if (threadIdx.x == 0 && blockIdx.x + blockIdx.y * gridDim.x < 8192)
+        g_pf_trace[8192 + blockIdx.x + blockIdx.y * gridDim.x] = make_uint4((unsigned) t_a, (unsigned) t_b, (unsigned) t_c, 0u);
+#endif
+
+    if (pslot >= 0) {                                     // a part: unnormalised partial
+        float * R = pbuf + (size_t) (pslot * LK_N_KV_HEADS + kvh) * PF_PART_SLOT;
+        lk_f4 * A = (lk_f4 *) R + (size_t) w * 16 * PF_BQ;                 // [16 chunks][64 rows]
+        float2 * ML = (float2 *) (R + PF_PART_ACC) + w * PF_BQ;           // [64 rows]
+#pragma unroll
+        for (int qb = 0; qb < PF_QB; ++qb) {
+            const int row = 16 * qb + col;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) A[(4 * db + g) * PF_BQ + row] = acc[db][qb];
+            if (g == 0) ML[row] = make_float2(mrun[qb] * sq[qb], acc[4][qb][0]);
+        }
+        trace_end(kt_hi - kt_lo);
+        return;
     }
 
     // ---- epilogue: l over the 4 lane groups, then o[q][head*64 + d] -------------
@@ -472,6 +581,62 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                     make_float4(a[0], a[1], a[2], a[3]);
             }
         }
+    }
+    trace_end(kt_hi - kt_lo);
+}
+
+// Merge of the parts of split query blocks: workgroup (split block, kv head,
+// quarter of the dims), thread = (head, row) over 16 dims; the parts are
+// weighted 2^(m_p - M) with the exact max M and summed in part order.  All of
+// a thread's loads are independent, so it waits for memory about twice.
+__global__ void __launch_bounds__(256)
+lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work, float * __restrict__ o) {
+    constexpr int MAXP = 8;                               // parts merged per pass
+    const int kvh = blockIdx.y, dq = blockIdx.z;          // dims 16dq .. 16dq+15
+    const int qt = work.split_qt[blockIdx.x];
+    int np, per;
+    pf_parts(qt, m, P, work.lsplit, np, per);
+    const int slot = work.slot0[qt];
+    const int row = threadIdx.x & 63, h = threadIdx.x >> 6;
+    const int qr = qt * PF_BQ + row;
+    if (qr >= m) return;
+    auto base = [&](int p) { return pbuf + (size_t) ((slot + p) * LK_N_KV_HEADS + kvh) * PF_PART_SLOT; };
+    float M = -INFINITY, L = 0.0f;
+    lk_f4 A[4] = {};
+    for (int p0 = 0; p0 < np; p0 += MAXP) {
+        float2 ml[MAXP];
+        lk_f4 a[MAXP][4];
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            const int p = (p0 + i < np) ? p0 + i : p0;    // clamped: loads stay in bounds
+            ml[i] = ((const float2 *) (base(p) + PF_PART_ACC))[h * PF_BQ + row];
+            const lk_f4 * src = (const lk_f4 *) base(p) + (size_t) (h * 16 + 4 * dq) * PF_BQ + row;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a[i][c] = src[c * PF_BQ];
+        }
+        float Mn = M;
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) if (p0 + i < np) Mn = fmaxf(Mn, ml[i].x);
+        const float r = lk_exp2(M - Mn);                  // 0 on the first pass (M = -inf)
+        L *= r;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) A[c] *= r;
+#pragma unroll
+        for (int i = 0; i < MAXP; ++i) {
+            if (p0 + i >= np) break;
+            const float wgt = lk_exp2(ml[i].x - Mn);
+            L += ml[i].y * wgt;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) A[c] += a[i][c] * wgt;
+        }
+        M = Mn;
+    }
+    const float il = 1.0f / L;
+    float * dst = o + (size_t) qr * LK_HIDDEN + (kvh * LK_G + h) * LK_HEAD_DIM + 16 * dq;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const lk_f4 v = A[c] * il;
+        *(float4 *) (dst + 4 * c) = make_float4(v[0], v[1], v[2], v[3]);
     }
 }
 
@@ -523,6 +688,119 @@ extern "C" int lk_pf_kmean(const void * kc, int n, float * cm, void * stream) {
     return lk_launch_status("lk_pf_kmean");
 }
 
+// ---- host: split choice -------------------------------------------------------
+// -1: never split, 0: automatic, > 0: parts of at most that many tiles (test hook)
+static int g_pf_split_override = 0;
+
+extern "C" int lk_pf_split_override(int tiles) {
+    if (tiles < -1) return lk_fail(hipErrorInvalidValue, "lk_pf_split_override: %d < -1", tiles);
+    g_pf_split_override = tiles;
+    return 0;
+}
+
+// Device address of the partial scratch, per device (looked up once).
+static float * pf_part_ptr(int & err) {
+    static float * ptr[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= 64) { err = lk_fail(e != hipSuccess ? (int) e : (int) hipErrorInvalidDevice, "prefill: no current device"); return nullptr; }
+    if (!ptr[dev]) {
+        void * p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_part));
+        if (e != hipSuccess) { err = lk_fail((int) e, "prefill: scratch lookup: %s", hipGetErrorString(e)); return nullptr; }
+        ptr[dev] = (float *) p;
+    }
+    err = 0;
+    return ptr[dev];
+}
+
+static int pf_slots_per_device() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return 2 * cus[dev];                                  // two attention workgroups per CU
+}
+
+// The work list of this chunk: n_items = 0 for an unsplit launch.
+static void pf_plan(int m, int P, PfWork & wk) {
+    wk.n_items = 0; wk.n_split = 0; wk.lsplit = 0;
+    const int nq = (m + PF_BQ - 1) / PF_BQ;
+    if (g_pf_split_override < 0 || nq > PF_MAX_QB) return;
+    long total = 0;
+    for (int qt = 0; qt < nq; ++qt) total += pf_nkt(qt, m, P);
+    const int nkt_max = pf_nkt(nq - 1, m, P);
+    int L;
+    if (g_pf_split_override > 0) L = g_pf_split_override;
+    else {
+        const long slots = pf_slots_per_device();
+        // target 1.5x the mean work per workgroup slot: finer parts measured
+        // slower (each workgroup pays a few microseconds of start-up)
+        L = (int) ((3 * total * LK_N_KV_HEADS + 2 * slots - 1) / (2 * slots));
+        if (L < 8) L = 8;
+        if (4 * nkt_max <= 5 * L) return;                 // longest block within 1.25x of the target
+    }
+    for (;; L *= 2) {
+        if (L >= nkt_max) return;
+        int items = 0, parts = 0, nsplit = 0;
+        for (int qt = 0; qt < nq; ++qt) {
+            int np, per;
+            pf_parts(qt, m, P, L, np, per);
+            items += np;
+            if (np > 1) { parts += np; ++nsplit; }
+        }
+        if (nsplit == 0) return;
+        if (items <= PF_MAX_ITEMS && (size_t) parts * LK_N_KV_HEADS * PF_PART_SLOT <= PF_PART_CAP) break;
+    }
+    // items longest first (ties: later block first), slots in block order
+    struct It { int size, qt, part; };
+    It list[PF_MAX_ITEMS];
+    int n = 0, slot = 0;
+    for (int qt = nq - 1; qt >= 0; --qt) {
+        int np, per;
+        pf_parts(qt, m, P, L, np, per);
+        const int nkt = pf_nkt(qt, m, P);
+        wk.slot0[qt] = (int16_t) (np > 1 ? slot : -1);
+        if (np > 1) { wk.split_qt[wk.n_split++] = (uint8_t) qt; slot += np; }
+        for (int p = 0; p < np; ++p) {
+            const int k0 = p * per, k1 = (k0 + per < nkt) ? k0 + per : nkt;
+            list[n++] = It{ k1 - k0, qt, p };
+        }
+    }
+    std::stable_sort(list, list + n, [](const It & a, const It & b) { return a.size > b.size; });
+    for (int i = 0; i < n; ++i) wk.item[i] = (uint16_t) (list[i].qt | (list[i].part << 8));
+    wk.n_items = n;
+    wk.lsplit = L;
+}
+
+template <bool INT8>
+static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qcs, const _Float16 * qh,
+                          int m, int P, const int8_t * k8, const float * ksc, int kstride,
+                          const _Float16 * kc, const _Float16 * vc, int near, int sink, float * o,
+                          hipStream_t st, const char * what) {
+    PfWork wk;
+    pf_plan(m, P, wk);
+    if (wk.n_items == 0) {
+        hipLaunchKernelGGL(lk_k_pf_attn<INT8>, dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0, st,
+                           q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, wk, (float *) nullptr);
+        return lk_launch_status(what);
+    }
+    int err = 0;
+    float * pbuf = pf_part_ptr(err);
+    if (!pbuf) return err;
+    hipLaunchKernelGGL(lk_k_pf_attn<INT8>, dim3(wk.n_items * LK_N_KV_HEADS), dim3(256), 0, st,
+                       q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, wk, pbuf);
+    int rc = lk_launch_status(what);
+    if (rc) return rc;
+    hipLaunchKernelGGL(lk_k_pf_combine, dim3(wk.n_split, LK_N_KV_HEADS, 4), dim3(256), 0, st,
+                       (const float *) pbuf, m, P, wk, o);
+    return lk_launch_status(what);
+}
+
 extern "C" int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * qcs,
                            const void * qh, int m, int P, const int8_t * k8,
                            const float * ksc, int kstride, const void * kc,
@@ -533,10 +811,9 @@ extern "C" int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * q
         return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: kstride %d must be a multiple of 4 and >= P+m %d", kstride, P + m);
     if (!q8 || !qsc || !qh || !k8 || !ksc || !kc || !vc || !o)
         return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: null pointer argument");
-    hipLaunchKernelGGL(lk_k_pf_attn<true>, dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0,
-                       lk_stream(stream), q8, qsc, qcs, (const _Float16 *) qh, m, P, k8, ksc, kstride,
-                       (const _Float16 *) kc, (const _Float16 *) vc, near, sink, o);
-    return lk_launch_status("lk_pf_attn8");
+    return pf_attn_launch<true>(q8, qsc, qcs, (const _Float16 *) qh, m, P, k8, ksc, kstride,
+                                (const _Float16 *) kc, (const _Float16 *) vc, near, sink, o,
+                                lk_stream(stream), "lk_pf_attn8");
 }
 
 extern "C" int lk_pf_attn(const void * qh, int m, int P, const void * kc, const void * vc,
@@ -544,11 +821,9 @@ extern "C" int lk_pf_attn(const void * qh, int m, int P, const void * kc, const 
     if (m < 0 || P < 0) return lk_fail(hipErrorInvalidValue, "lk_pf_attn: m %d / P %d negative", m, P);
     if (m == 0) return 0;
     if (!qh || !kc || !vc || !o) return lk_fail(hipErrorInvalidValue, "lk_pf_attn: null pointer argument");
-    hipLaunchKernelGGL(lk_k_pf_attn<false>, dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0,
-                       lk_stream(stream), (const int8_t *) nullptr, (const float *) nullptr,
-                       (const float *) nullptr, (const _Float16 *) qh, m, P, (const int8_t *) nullptr,
-                       (const float *) nullptr, 0, (const _Float16 *) kc, (const _Float16 *) vc, 0, 0, o);
-    return lk_launch_status("lk_pf_attn");
+    return pf_attn_launch<false>(nullptr, nullptr, nullptr, (const _Float16 *) qh, m, P, nullptr, nullptr, 0,
+                                 (const _Float16 *) kc, (const _Float16 *) vc, 0, 0, o,
+                                 lk_stream(stream), "lk_pf_attn");
 }
 
 extern "C" int lk_pf_qk_i32(const int8_t * q8, int m, const int8_t * k8, int n,

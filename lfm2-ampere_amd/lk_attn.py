@@ -28,7 +28,8 @@ EXPORTS = (
     "lk_attn_split", "lk_attn_combine", "lk_attn_decode", "lk_attention_decode",
     "lk_decode_graph_create", "lk_decode_graph_launch", "lk_decode_graph_nodes",
     "lk_decode_graph_destroy",
-    "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_qk_i32",
+    "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_split_override",
+    "lk_pf_qk_i32",
 )
 
 
@@ -67,6 +68,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_kmean": ([P, I, P, P], I),
         "lk_pf_attn8": ([P, P, P, P, I, I, P, P, I, P, P, I, I, P, P], I),
         "lk_pf_attn": ([P, I, I, P, P, P, P], I),
+        "lk_pf_split_override": ([I], I),
         "lk_pf_qk_i32": ([P, I, P, I, P, P], I),
     }
     for name, (args, res) in sig.items():
@@ -208,6 +210,11 @@ def pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, st
 
 def pf_attn(qh, m, P, kc, vc, o, stream=None) -> None:
     _check(load().lk_pf_attn(_ptr(qh), m, P, _ptr(kc), _ptr(vc), _ptr(o), _stream(stream)), "lk_pf_attn")
+
+
+def pf_split_override(tiles: int) -> None:
+    """-1 never split prefill blocks, 0 automatic, n > 0 parts of <= n key tiles."""
+    _check(load().lk_pf_split_override(int(tiles)), "lk_pf_split_override")
 
 
 def pf_qk_i32(q8, m, k8, n, s, stream=None) -> None:

@@ -55,6 +55,8 @@ def test_host_argument_errors():
     assert lib.lk_pf_attn8(p, p, p, p, 10, 0, p, p, 8, p, p, 0, 0, p, None) == 1   # kstride < P+m
     assert lib.lk_pf_qk_i32(p, 17, p, 16, p, None) == 1
     assert lib.lk_pf_kmean(p, 0, p, None) == 1
+    assert lib.lk_pf_split_override(-2) == 1
+    assert lib.lk_pf_split_override(0) == 0
     # empty work is a successful no-op
     assert lib.lk_pf_q8(None, 0, None, None, None, None, None) == 0
     assert lib.lk_pf_attn(None, 0, 0, None, None, None, None) == 0

@@ -189,6 +189,43 @@ def test_attn8_deterministic(lk, oracle):
         assert np.array_equal(d.attn8(lk, 128, 1).view(np.uint32), a.view(np.uint32))
 
 
+# ---- split-K work items (forced part sizes) --------------------------------------------------
+SPLIT_CASES = [
+    # (m, P, near, tiles per part)
+    (300, 0, 96, 1),
+    (300, 700, 96, 2),
+    (129, 2000, 1024, 5),
+    (500, 0, 0, 3),
+    (64, 0, 0, 1),
+]
+
+
+@pytest.mark.parametrize("m,P,near,L", SPLIT_CASES, ids=[f"m{c[0]}_P{c[1]}_n{c[2]}_L{c[3]}" for c in SPLIT_CASES])
+def test_attn_split_parts(lk, oracle, m, P, near, L):
+    K, V, Q = _inputs(oracle, m, P, 1.0, True)
+    sink = int(near > 0)
+    note(f"pf split parts m={m} P={P} near={near} L={L}")
+    d = _Dev(lk, K, V, Q, m, P, False)
+    try:
+        lk.pf_split_override(-1)
+        whole8, whole16 = d.attn8(lk, near, sink), d.attn16(lk)
+        lk.pf_split_override(L)
+        part8, part16 = d.attn8(lk, near, sink), d.attn16(lk)
+        again8 = d.attn8(lk, near, sink)
+    finally:
+        lk.pf_split_override(0)
+    ref8 = oracle.pf_ref8(host(d.q8), host(d.qsc), host(d.qcs), Q, m, P, host(d.k8), host(d.ksc),
+                          d.kstride, K, V, near, sink)
+    ref = oracle.pf_ref(Q, m, P, K, V)
+    r8, r16 = oracle.rel_err(part8, ref8), oracle.rel_err(part16, ref)
+    d8, d16 = oracle.rel_err(part8, whole8), oracle.rel_err(part16, whole16)
+    note(f"  split: int8 rel {r8:.3e}, fp16 rel {r16:.3e}; vs unsplit rel {d8:.3e} / {d16:.3e}")
+    assert r8 <= 2e-3 and r16 <= 2e-3 and abs_err(part16, ref) <= 4e-3
+    # parts round p against their own running max: same tolerance class as above
+    assert d8 <= 1e-3 and d16 <= 1e-3
+    assert np.array_equal(again8.view(np.uint32), part8.view(np.uint32))
+
+
 # ---- BASELINE prefill configurations (sampled rows against the float64 oracle) -----------------
 def _config_rows(m, long_ctx):
     rows = {0, 63, 64, 1023, m - 1} if long_ctx else \
