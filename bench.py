@@ -134,10 +134,12 @@ def bench_prefill_c4(lk, lkc, iters):
     q_ms = timed_events(lambda: lk.pf_q8(qh, m, None, q8, qsc, qcs, stream=st), st, iters)
     k_ms = timed_events(lambda: lk.pf_k8(kc, 0, S, None, ks, k8, ksc, stream=st), st, iters)
     f8 = lambda: lk.pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
-    f8()
+    for _ in range(iters):                  # warm-up (clocks settle over the first ~100 us)
+        f8()
     a8_ms = timed_events(f8, st, iters)
     f16 = lambda: lk.pf_attn(qh, m, P, kc, vc, o, stream=st)
-    f16()
+    for _ in range(iters):
+        f16()
     a16_ms = timed_events(f16, st, iters)
     oi, of, pairs = pf_ops(m, P)
     peak_ms = (oi / (PEAK_INT8_TOPS * 1e12) + of / (PEAK_FP16_TFLOPS * 1e12)) * 1e3
@@ -221,6 +223,34 @@ def cpu_baseline(seconds):
     return res
 
 
+def profile_prefill(lk, lkc, which, launches):
+    """For rocprofv3 --pmc runs: `launches` int8 prefill attention launches on
+    C4 (the 4096 chunk at P = 0) or on C5's last chunk (P = 126976)."""
+    import torch
+    if which == "c4":
+        qh, kc, vc, S = lkc.prefill_inputs("C4")
+        m, P, qc = S, 0, qh
+    else:
+        qh, kc, vc, S = lkc.prefill_inputs("C5")
+        m, P = 4096, S - 4096
+        qc = qh[P:].contiguous()
+    ks = lk.kstride_for(P + m)
+    q8 = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
+    qsc = torch.empty(m, 32, device="cuda")
+    qcs = torch.empty(m, 32, device="cuda")
+    k8 = torch.empty((P + m) * 512, dtype=torch.int8, device="cuda")
+    ksc = torch.empty(8 * ks + 4, device="cuda")
+    o = torch.empty(m, 2048, device="cuda")
+    lk.pf_q8(qc, m, None, q8, qsc, qcs)
+    lk.pf_k8(kc, 0, P + m, None, ks, k8, ksc)
+    for _ in range(launches):
+        lk.pf_attn8(q8, qsc, qcs, qc, m, P, k8, ksc, ks, kc, vc, 1024, 1, o)
+    torch.cuda.synchronize()
+    oi, of, pairs = pf_ops(m, P)
+    log(f"profile: {launches} prefill attention launches ({which}, m {m}, P {P}, "
+        f"{pairs:.0f} (query, key) pairs, {oi + of:.4g} algorithmic ops each)")
+
+
 def profile_decode_split(lk, lkc, launches):
     """For rocprofv3 --pmc runs: `launches` back-to-back lk_attn_split launches
     on C2 (rotating over 10 distinct 67 MB caches), then one 1 GiB device copy
@@ -253,6 +283,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile-split", type=int, default=0,
                     help="only run N C2 split launches + a 1 GiB copy (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-prefill", choices=["c4", "c5"], default=None,
+                    help="only run --profile-launches int8 prefill attention launches (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-launches", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this attention path is built and measured on a single "
@@ -267,6 +300,9 @@ def main():
     cfgp = lk.config()
     if args.profile_split:
         profile_decode_split(lk, lkc, args.profile_split)
+        return
+    if args.profile_prefill:
+        profile_prefill(lk, lkc, args.profile_prefill, args.profile_launches)
         return
 
     log("decode C2 (32k x 10 layers, one hipGraph)")

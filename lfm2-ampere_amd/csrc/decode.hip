@@ -8,21 +8,18 @@
 // for the 32 query heads, K/V of kv head h/4 in the fp16 cache [pos][8][64].
 //
 // MI355X design (not a translation of the reference's warp-level loops):
-//   * grid (8 kv heads x LK_ATTN_SPLIT slices) of 4-wave workgroups; a
-//     workgroup streams its kv head's K and V slice exactly once for the four
-//     query heads sharing it (algorithmic traffic: seq x 2 KB per layer);
-//   * each wave takes 16-token groups; lane l loads 32 contiguous bytes
-//     (dims 16g..16g+15 of token l%16, g = l/16) of K and of V with two
-//     128-bit loads, LK_ATTN_UNROLL groups in flight before any is consumed;
-//   * Q.K^T runs on the matrix cores: v_mfma_f32_16x16x32_f16 with the four
-//     heads' q replicated over the 16 A rows, so every lane receives the four
-//     heads' scores of its own token.  q is fp32 in the interface, so it is
-//     split q = hi + lo into two fp16 halves (22 significant bits) and both
-//     halves are multiplied (fp16 x fp16 products are exact in fp32);
-//   * online softmax in the log2 domain per wave (v_exp_f32), P.V on the VALU
-//     in fp32 (fma with fp16 V operands), then a fixed butterfly over the 16
-//     token lanes and a fixed wave order in LDS -> one partial (m, l, acc[64])
-//     per (query head, slice);
+//   * grid of LK_ATTN_SPLIT 8-wave workgroups, one per contiguous slice of
+//     positions covering ALL 8 kv heads: whole 1 KB cache rows are streamed
+//     once into LDS by LDS DMA (algorithmic traffic: seq x 2 KB per layer);
+//     wave w then serves kv head w and its 4 query heads;
+//   * S^T = K . q^T on the matrix cores (v_mfma_f32_16x16x32_f16, keys as the
+//     A operand).  q is fp32 in the interface, so it is split q = hi + lo into
+//     two fp16 halves (22 significant bits; fp16 x fp16 products are exact in
+//     fp32) and both halves are multiplied;
+//   * online softmax in the log2 domain (v_exp_f32) with a lazily raised max;
+//   * O^T += V^T . P^T on the matrix cores (v_mfma_f32_16x16x16_f16, V^T from
+//     transposed LDS reads, P as hi + lo fp16 halves), l from an all-ones
+//     operand -> one partial (m, l, acc[64]) per (query head, slice);
 //   * the combine merges the slice partials in a fixed order (deterministic,
 //     run-to-run bit-identical) and optionally emits Q8_1 blocks.
 #include "lk_common.h"
