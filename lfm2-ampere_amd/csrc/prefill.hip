@@ -31,42 +31,70 @@
 #include <algorithm>
 
 // ---------------------------------------------------------------------------
-// int8 quantisers.  One wave per 64-wide (row, head), one value per lane.
+// int8 quantisers.  Eight lanes per 64-wide (row, head), eight consecutive
+// values per lane (one 16-byte load, one 8-byte store), eight rows per wave.
 // am = max|v| (exact: a maximum does not depend on order); d = am/127 and
 // 127/am are IEEE-correct fp32 divisions; q = round-to-nearest-even(v * id)
 // (reference prefill.cu:1255-1267).  Bit-exact by construction.
-__device__ __forceinline__ void lk_q8_row(float v, int8_t * __restrict__ dst,
-                                          float * __restrict__ scl, float mul) {
+__device__ __forceinline__ float lk_max8(float v) {     // max over the 8-lane group
+    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR1>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR2>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_HMIRROR>(v));
+    return v;
+}
+__device__ __forceinline__ void lk_q8_row8(const float (&v)[8], int8_t * __restrict__ dst8,
+                                           float * __restrict__ scl, float mul, bool lead) {
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    float am = fabsf(v);
+    float am = fabsf(v[0]);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    for (int i = 1; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+    am = lk_max8(am);
     const float d = am / 127.0f;
     const float id = (am > 0.0f) ? 127.0f / am : 0.0f;
-    const float x = v * id;
-    dst[lane] = (int8_t) (int) __builtin_rintf(x);
-    if (lane == 0) *scl = d * mul;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w0 |= (uint32_t) (uint8_t) (int8_t) (int) __builtin_rintf(v[i] * id) << (8 * i);
+        w1 |= (uint32_t) (uint8_t) (int8_t) (int) __builtin_rintf(v[4 + i] * id) << (8 * i);
+    }
+    *(uint2 *) dst8 = make_uint2(w0, w1);
+    if (lead) *scl = d * mul;
+}
+__device__ __forceinline__ void lk_load8h(const _Float16 * __restrict__ src, float (&v)[8]) {
+    const lk_h8 h = *(const lk_h8 *) src;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float) h[i];
 }
 
 // Q: qh fp16 [m][2048] -> q8 [m][2048], qsc [m][32] = d*log2(e), qcs [m][32] =
-// (q.c)*log2(e) where q.c is the lane products v_d*c_d summed by an xor
-// butterfly 32,16,8,4,2,1 (fixed order), or 0 without cm.
+// (q.c)*log2(e), or 0 without cm.  q.c = sum over d of v_d*c_d by the xor
+// butterfly over d with strides 32, 16, 8, 4, 2, 1 (fixed order): the first
+// three strides pair lanes of the group (xor 4, 2, 1), the last three pair
+// values inside a lane.
 __global__ void __launch_bounds__(256)
 lk_k_pf_q8(const _Float16 * __restrict__ qh, int m, const float * __restrict__ cm,
            int8_t * __restrict__ q8, float * __restrict__ qsc, float * __restrict__ qcs) {
 #pragma clang fp contract(off)
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (r >= m * LK_N_HEADS) return;                      // wave-uniform
-    const float v = (float) qh[(size_t) r * LK_HEAD_DIM + lane];
-    lk_q8_row(v, q8 + (size_t) r * LK_HEAD_DIM, qsc + r, LK_LOG2E_F);
+    const int r = blockIdx.x * 32 + (threadIdx.x >> 3), j = threadIdx.x & 7;
+    if (r >= m * LK_N_HEADS) return;                      // whole 8-lane groups
+    float v[8];
+    lk_load8h(qh + (size_t) r * LK_HEAD_DIM + 8 * j, v);
+    lk_q8_row8(v, q8 + (size_t) r * LK_HEAD_DIM + 8 * j, qsc + r, LK_LOG2E_F, j == 0);
     float qc = 0.0f;
     if (cm) {
-        qc = v * cm[((r % LK_N_HEADS) / LK_G) * LK_HEAD_DIM + lane];
+        const float * c = cm + ((r % LK_N_HEADS) / LK_G) * LK_HEAD_DIM + 8 * j;
+        float t[8];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) qc += __shfl_xor(qc, o, 64);
+        for (int i = 0; i < 8; ++i) t[i] = v[i] * c[i];
+#pragma unroll
+        for (int o = 4; o > 0; o >>= 1)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t[i] += __shfl_xor(t[i], o, 64);
+        const float u0 = t[0] + t[4], u1 = t[1] + t[5], u2 = t[2] + t[6], u3 = t[3] + t[7];
+        const float w0 = u0 + u2, w1 = u1 + u3;
+        qc = w0 + w1;
     }
-    if (lane == 0) qcs[r] = qc * LK_LOG2E_F;
+    if (j == 0) qcs[r] = qc * LK_LOG2E_F;
 }
 
 // K: positions [p0, p1) of kc [pos][8][64] -> k8 (same layout), ksc[h][pos].
@@ -74,13 +102,17 @@ __global__ void __launch_bounds__(256)
 lk_k_pf_k8(const _Float16 * __restrict__ kc, int p0, int p1, const float * __restrict__ cm,
            int kstride, int8_t * __restrict__ k8, float * __restrict__ ksc) {
 #pragma clang fp contract(off)
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 32 + (threadIdx.x >> 3), j = threadIdx.x & 7;
     const int pos = p0 + r / LK_N_KV_HEADS, h = r % LK_N_KV_HEADS;
-    if (pos >= p1) return;                                // wave-uniform
+    if (pos >= p1) return;                                // whole 8-lane groups
     const size_t row = (size_t) pos * LK_N_KV_HEADS + h;
-    float v = (float) kc[row * LK_HEAD_DIM + lane];
-    if (cm) v -= cm[h * LK_HEAD_DIM + lane];
-    lk_q8_row(v, k8 + row * LK_HEAD_DIM, ksc + (size_t) h * kstride + pos, 1.0f);
+    float v[8];
+    lk_load8h(kc + row * LK_HEAD_DIM + 8 * j, v);
+    if (cm) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] -= cm[h * LK_HEAD_DIM + 8 * j + i];
+    }
+    lk_q8_row8(v, k8 + row * LK_HEAD_DIM + 8 * j, ksc + (size_t) h * kstride + pos, 1.0f, j == 0);
 }
 
 // cm[h][d] = mean of kc over positions [0, n).  The summation order is the
@@ -662,7 +694,7 @@ extern "C" int lk_pf_q8(const void * qh, int m, const float * cm, int8_t * q8,
     if (m == 0) return 0;
     if (!qh || !q8 || !qsc || !qcs) return lk_fail(hipErrorInvalidValue, "lk_pf_q8: null pointer argument");
     const int rows = m * LK_N_HEADS;
-    hipLaunchKernelGGL(lk_k_pf_q8, dim3((rows + 3) / 4), dim3(256), 0, lk_stream(stream),
+    hipLaunchKernelGGL(lk_k_pf_q8, dim3((rows + 31) / 32), dim3(256), 0, lk_stream(stream),
                        (const _Float16 *) qh, m, cm, q8, qsc, qcs);
     return lk_launch_status("lk_pf_q8");
 }
@@ -675,7 +707,7 @@ extern "C" int lk_pf_k8(const void * kc, int p0, int p1, const float * cm, int k
     if (p1 == p0) return 0;
     if (!kc || !k8 || !ksc) return lk_fail(hipErrorInvalidValue, "lk_pf_k8: null pointer argument");
     const long rows = (long) (p1 - p0) * LK_N_KV_HEADS;
-    hipLaunchKernelGGL(lk_k_pf_k8, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, lk_stream(stream),
+    hipLaunchKernelGGL(lk_k_pf_k8, dim3((unsigned) ((rows + 31) / 32)), dim3(256), 0, lk_stream(stream),
                        (const _Float16 *) kc, p0, p1, cm, kstride, k8, ksc);
     return lk_launch_status("lk_pf_k8");
 }
