@@ -199,10 +199,63 @@ def bench_prefill_c5(lk, lkc, reps):
     }
 
 
-def cpu_baseline(seconds):
-    """The oracle's float64 decode attention (the reference's CPU path,
-    tests/test_attn.cu:46-74), single-threaded, on C2 (ctx 32768) and C1."""
+def bench_producers(lk, iters):
+    """The attention-input producers (reference kernels.cu:871-915,
+    prefill.cu:975-1016): the prefill pass over one 4096-token chunk (C4's
+    shape) with and without the fused int8 K copy, against qknr + pf_k8 as two
+    passes, and the decode kernel for one token.  HBM-bound; algorithmic bytes
+    = Y read (m x 3072 fp32) + qh, K, V written (fp16) [+ int8 K and scales]."""
+    import torch
+    m, P = 4096, 0
+    S = P + m
+    ks = lk.kstride_for(S)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    Y = torch.randn(m, 3072, device="cuda", generator=g) * 3.0
+    qn = torch.rand(64, device="cuda", generator=g) + 0.5
+    kn = torch.rand(64, device="cuda", generator=g) + 0.5
+    qh = torch.empty(m, 2048, dtype=torch.float16, device="cuda")
+    kc = torch.empty(S, 8, 64, dtype=torch.float16, device="cuda")
+    vc = torch.empty_like(kc)
+    k8 = torch.empty(S * 512, dtype=torch.int8, device="cuda")
+    ksc = torch.empty(8 * ks + 4, device="cuda")
+    st = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    f0 = lambda: lk.pf_qknr(Y, qn, kn, m, P, qh, kc, vc, stream=st)
+    f1 = lambda: lk.pf_qknr(Y, qn, kn, m, P, qh, kc, vc, k8, ksc, ks, stream=st)
+    f2 = lambda: (lk.pf_qknr(Y, qn, kn, m, P, qh, kc, vc, stream=st),
+                  lk.pf_k8(kc, P, S, None, ks, k8, ksc, stream=st))
+    for f in (f0, f1, f2):
+        for _ in range(iters):
+            f()
+    t0 = timed_events(f0, st, iters)
+    t1 = timed_events(f1, st, iters)
+    t2 = timed_events(f2, st, iters)
+    b0 = m * 3072 * 4 + m * 2048 * 2 + m * 512 * 2 * 2
+    b1 = b0 + m * 512 + m * 8 * 4
+    qf = torch.randn(2048, device="cuda", generator=g)
+    kf = torch.randn(512, device="cuda", generator=g)
+    vf = torch.randn(512, device="cuda", generator=g)
+    d_pos = torch.tensor([S - 1], dtype=torch.int32, device="cuda")
+    fd = lambda: lk.qk_norm_rope(qf, kf, vf, qn, kn, d_pos, kc, vc, stream=st)
+    for _ in range(iters):
+        fd()
+    td = timed_events(fd, st, iters)
+    return {
+        "m": m, "qknr_us": t0 * 1e3, "qknr_GBps": b0 / (t0 * 1e-3) / 1e9, "qknr_bytes": b0,
+        "qknr_k8_fused_us": t1 * 1e3, "qknr_k8_fused_GBps": b1 / (t1 * 1e-3) / 1e9,
+        "qknr_then_k8_us": t2 * 1e3, "decode_qk_norm_rope_us": td * 1e3,
+    }
+
+
+def cpu_baseline(seconds, prefill=True):
+    """The reference's CPU path restated in the oracle (float64, single
+    thread): decode attention (tests/test_attn.cu:46-74) on a full C2 layer and
+    on C1, and prefill attention (tests/test_prefill.cu:263-282) on sampled
+    query rows of C4 and of C5's last chunk, extrapolated by the number of
+    (query, key) pairs to the whole chunk / prompt."""
     import numpy as np
+    import torch
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import lk_oracle as orc
     import lk_configs as lkc
@@ -210,8 +263,8 @@ def cpu_baseline(seconds):
     for cfg, budget in (("C2", seconds), ("C1", max(2.0, seconds / 5))):
         qs, kcs, vcs, seq = lkc.decode_inputs(cfg, layers=1)
         q = qs[0].cpu().numpy()
-        kh = kcs[0].view(__import__("torch").int16).cpu().numpy().view(np.uint16)
-        vh = vcs[0].view(__import__("torch").int16).cpu().numpy().view(np.uint16)
+        kh = kcs[0].view(torch.int16).cpu().numpy().view(np.uint16)
+        vh = vcs[0].view(torch.int16).cpu().numpy().view(np.uint16)
         n, t0 = 0, time.perf_counter()
         while True:
             orc.decode_ref(q, kh, vh, seq)
@@ -220,6 +273,31 @@ def cpu_baseline(seconds):
                 break
         dt = (time.perf_counter() - t0) / n
         res[cfg] = {"us_per_layer": dt * 1e6, "GBps": seq * 2048.0 / dt / 1e9, "reps": n}
+    if not prefill:
+        return res
+    h16 = lambda t: t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    for cfg, nrows in (("C4", 48), ("C5", 2)):
+        qh, kc, vc, S = lkc.prefill_inputs(cfg)
+        m = 4096
+        P = 0 if cfg == "C4" else S - m
+        rows = np.linspace(0, m - 1, nrows).astype(np.int32)
+        Q, K, V = h16(qh[P:P + m]), h16(kc[:P + m]), h16(vc[:P + m])
+        del qh, kc, vc
+        t0 = time.perf_counter()
+        orc.pf_ref(Q, m, P, K, V, rows=rows)
+        dt = time.perf_counter() - t0
+        pairs_s = 32.0 * float(np.sum(P + rows.astype(np.float64) + 1))
+        if cfg == "C4":
+            pairs_full = pf_ops(m, 0)[2]
+        else:
+            pairs_full = sum(pf_ops(m, p)[2] for p in range(0, S, m))
+        tf = dt * pairs_full / pairs_s
+        ops = pairs_full * 256.0
+        res[cfg] = {"s_extrapolated": tf, "TOPS": ops / tf / 1e12, "sample_rows": int(nrows),
+                    "sample_s": dt, "sample_pairs": pairs_s,
+                    "note": "float64 reference on sampled query rows (all 32 heads), "
+                            "extrapolated by (query, key) pairs"}
+        torch.cuda.empty_cache()
     return res
 
 
@@ -319,16 +397,20 @@ def main():
         log("prefill C5 (131072 prompt, 32 chunks)")
         results["C5_prefill_131k"] = bench_prefill_c5(lk, lkc, 2)
         log(json.dumps(results["C5_prefill_131k"]))
+        log("attention-input producers (qk norm + rope + cache write)")
+        results["producers"] = bench_producers(lk, 20)
+        log(json.dumps(results["producers"]))
 
     cpu = None
     if not args.skip_cpu:
         log("cpu baseline (float64 oracle, 1 thread)")
-        cb = cpu_baseline(args.cpu_seconds)
+        cb = cpu_baseline(args.cpu_seconds, prefill=not args.skip_prefill)
         results["cpu_float64"] = cb
         cpu = {"value": cb["C2"]["GBps"], "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": f"full C2 layer (32q/8kv/64, ctx 32768) float64 decode attention, "
                          f"{cb['C2']['reps']} repetitions, {cb['C2']['us_per_layer']:.0f} us/layer; "
-                         f"host nproc {os.cpu_count()}"}
+                         f"host nproc {os.cpu_count()}; prefill CPU figures (sampled rows, "
+                         f"extrapolated) under results.cpu_float64"}
 
     ach = c2["split_GBps"]
     line = {

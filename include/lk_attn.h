@@ -162,6 +162,37 @@ int lk_pf_attn(const void * qh, int m, int P, const void * kc, const void * vc,
  * split). */
 int lk_pf_split_override(int tiles);
 
+/* ---- attention-input producers ---------------------------------------------
+ * Per-head RMS norm (eps 1e-5) of q and k with weights qn / kn (fp32 [64]),
+ * NEOX rotary embedding (theta 1e7) at the token's position, and the fp16
+ * KV-cache write [pos][8][64].  1/sqrt, theta^(-i/32) and the cos/sin of the
+ * fp32 angle are correctly rounded fp32 values (the reference uses CUDA's
+ * rsqrtf / powf / sincosf). */
+
+/* Replaces k_qk_norm_rope (reference kernels.cuh:666-670, kernels.cu:871-915;
+ * launched at engine.cu:606-608):
+ * qf fp32 [32][64] and kf fp32 [8][64] are normalised and rotated in place at
+ * position *d_pos (device int32, graph-capturable); K and vf fp32 [8][64] go
+ * to row *d_pos of kc / vc. */
+int lk_qk_norm_rope(float * qf, float * kf, const float * vf, const float * qn,
+                    const float * kn, const int * d_pos, void * kc, void * vc,
+                    void * stream);
+
+/* Replaces k_pf_qknr (reference prefill.cuh:85-87, prefill.cu:975-1016;
+ * launched at engine.cu:1069-1070):
+ * Y fp32 [m][3072] (q | k | v projection rows) for positions P .. P+m-1 ->
+ * qh fp16 [m][2048] (rotated q x 1/8), K and V into rows P .. P+m-1 of kc / vc.
+ * With k8 != NULL the same pass also writes the int8 copy of those K rows
+ * (k8 [pos][8][64], ksc [8][kstride], kstride a multiple of 4 and >= P+m),
+ * byte-identical to lk_pf_k8 over [P, P+m) with the same cm (NULL: none) --
+ * the new rows of the reference's separate k_pf_k8 pass (engine.cu:1082-1083)
+ * fused away.  Keys written by decode steps since the last prefill, and a
+ * first chunk whose smoothing vector is derived from these very keys, still
+ * need lk_pf_k8 / lk_pf_kmean. */
+int lk_pf_qknr(const float * Y, const float * qn, const float * kn, int m, int P,
+               void * qh, void * kc, void * vc, int8_t * k8, float * ksc, int kstride,
+               const float * cm, void * stream);
+
 /* ---- test hook --------------------------------------------------------------
  * The raw int32 Q.K^T sums of the int8 scoring path, computed by the same
  * matrix-core routine lk_pf_attn8 uses:  s[head][i][j] = sum_d q8[i][head][d] *

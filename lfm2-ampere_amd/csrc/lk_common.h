@@ -130,6 +130,38 @@ __host__ __device__ __forceinline__ void lk_attn_slices(int seq, int & ns, int &
     chunk = (seq + s - 1) / s;
 }
 
+// ---- int8 row quantiser on 8-lane groups (shared by prefill.hip, qknr.hip) -----
+// A 64-wide row is held by 8 consecutive lanes, 8 consecutive values each.
+__device__ __forceinline__ float lk_max8(float v) {     // max over the 8-lane group
+    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR1>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR2>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_HMIRROR>(v));
+    return v;
+}
+__device__ __forceinline__ void lk_q8_row8(const float (&v)[8], int8_t * __restrict__ dst8,
+                                           float * __restrict__ scl, float mul, bool lead) {
+#pragma clang fp contract(off)
+    float am = fabsf(v[0]);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
+    am = lk_max8(am);
+    const float d = am / 127.0f;
+    const float id = (am > 0.0f) ? 127.0f / am : 0.0f;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        w0 |= (uint32_t) (uint8_t) (int8_t) (int) __builtin_rintf(v[i] * id) << (8 * i);
+        w1 |= (uint32_t) (uint8_t) (int8_t) (int) __builtin_rintf(v[4 + i] * id) << (8 * i);
+    }
+    *(uint2 *) dst8 = make_uint2(w0, w1);
+    if (lead) *scl = d * mul;
+}
+__device__ __forceinline__ void lk_load8h(const _Float16 * __restrict__ src, float (&v)[8]) {
+    const lk_h8 h = *(const lk_h8 *) src;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float) h[i];
+}
+
 // ---- LDS DMA (global_load_lds_dwordx4) --------------------------------------
 // Byte address of an LDS object (the value M0 takes for an LDS DMA).
 __device__ __forceinline__ uint32_t lk_lds_addr(const void * p) {

@@ -35,36 +35,8 @@
 // values per lane (one 16-byte load, one 8-byte store), eight rows per wave.
 // am = max|v| (exact: a maximum does not depend on order); d = am/127 and
 // 127/am are IEEE-correct fp32 divisions; q = round-to-nearest-even(v * id)
-// (reference prefill.cu:1255-1267).  Bit-exact by construction.
-__device__ __forceinline__ float lk_max8(float v) {     // max over the 8-lane group
-    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR1>(v));
-    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR2>(v));
-    v = fmaxf(v, lk_dpp<LK_DPP_HMIRROR>(v));
-    return v;
-}
-__device__ __forceinline__ void lk_q8_row8(const float (&v)[8], int8_t * __restrict__ dst8,
-                                           float * __restrict__ scl, float mul, bool lead) {
-#pragma clang fp contract(off)
-    float am = fabsf(v[0]);
-#pragma unroll
-    for (int i = 1; i < 8; ++i) am = fmaxf(am, fabsf(v[i]));
-    am = lk_max8(am);
-    const float d = am / 127.0f;
-    const float id = (am > 0.0f) ? 127.0f / am : 0.0f;
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        w0 |= (uint32_t) (uint8_t) (int8_t) (int) __builtin_rintf(v[i] * id) << (8 * i);
-        w1 |= (uint32_t) (uint8_t) (int8_t) (int) __builtin_rintf(v[4 + i] * id) << (8 * i);
-    }
-    *(uint2 *) dst8 = make_uint2(w0, w1);
-    if (lead) *scl = d * mul;
-}
-__device__ __forceinline__ void lk_load8h(const _Float16 * __restrict__ src, float (&v)[8]) {
-    const lk_h8 h = *(const lk_h8 *) src;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (float) h[i];
-}
+// (reference prefill.cu:1255-1267).  Bit-exact by construction.  The row
+// helpers (lk_q8_row8, lk_max8, lk_load8h) live in lk_common.h.
 
 // Q: qh fp16 [m][2048] -> q8 [m][2048], qsc [m][32] = d*log2(e), qcs [m][32] =
 // (q.c)*log2(e), or 0 without cm.  q.c = sum over d of v_d*c_d by the xor

@@ -29,7 +29,7 @@ EXPORTS = (
     "lk_decode_graph_create", "lk_decode_graph_launch", "lk_decode_graph_nodes",
     "lk_decode_graph_destroy",
     "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_split_override",
-    "lk_pf_qk_i32",
+    "lk_pf_qk_i32", "lk_qk_norm_rope", "lk_pf_qknr",
 )
 
 
@@ -70,6 +70,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_attn": ([P, I, I, P, P, P, P], I),
         "lk_pf_split_override": ([I], I),
         "lk_pf_qk_i32": ([P, I, P, I, P, P], I),
+        "lk_qk_norm_rope": ([P, P, P, P, P, P, P, P, P], I),
+        "lk_pf_qknr": ([P, P, P, I, I, P, P, P, P, P, I, P, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -224,3 +226,14 @@ def pf_qk_i32(q8, m, k8, n, s, stream=None) -> None:
 def kstride_for(S: int) -> int:
     """ksc row stride for S positions: rounded up to 4 (reference engine.cu:979)."""
     return (S + 3) & ~3
+
+
+# ---- attention-input producers (reference kernels.cu:871-915, prefill.cu:975-1016) ----
+def qk_norm_rope(qf, kf, vf, qn, kn, d_pos, kc, vc, stream=None) -> None:
+    _check(load().lk_qk_norm_rope(_ptr(qf), _ptr(kf), _ptr(vf), _ptr(qn), _ptr(kn), _ptr(d_pos),
+                                  _ptr(kc), _ptr(vc), _stream(stream)), "lk_qk_norm_rope")
+
+
+def pf_qknr(Y, qn, kn, m, P, qh, kc, vc, k8=None, ksc=None, kstride=0, cm=None, stream=None) -> None:
+    _check(load().lk_pf_qknr(_ptr(Y), _ptr(qn), _ptr(kn), int(m), int(P), _ptr(qh), _ptr(kc), _ptr(vc),
+                             _ptr(k8), _ptr(ksc), int(kstride), _ptr(cm), _stream(stream)), "lk_pf_qknr")

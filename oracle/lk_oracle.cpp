@@ -427,6 +427,77 @@ void lko_mt_prefill_case(uint32_t seed, int m, int P, float koff, int with_off,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Attention-input producers: per-head RMS norm + NEOX rotary embedding of one
+// 64-wide row (reference kernels.cu:886-910 and prefill.cu:989-1009, identical
+// arithmetic in both): ss = sum v^2 by the kernels' tree (d with d+32, then
+// +16, ..., +1), inv = 1/sqrt(ss/64 + 1e-5), y = (v*inv)*w, angle a_i =
+// (float)pos * theta^(-i/32) in fp32, then y_i c - y_{i+32} s and
+// y_i s + y_{i+32} c.  The reference evaluates rsqrtf / powf / sincosf with
+// CUDA's approximations; this restatement uses the correctly rounded fp32
+// values of 1/sqrt, theta^(-i/32), cos and sin (computed in double, rounded
+// once), the arithmetic the MI355X kernel implements.
+void lko_norm_rope_row(const float * v, const float * w, int pos, float * out) {
+    float a[64];
+    for (int d = 0; d < 64; ++d) a[d] = v[d] * v[d];
+    for (int o = 32; o > 0; o >>= 1)
+        for (int d = 0; d < o; ++d) a[d] = a[d] + a[d + o];
+    const float arg = a[0] * (1.0f / 64.0f) + 1e-5f;
+    const float inv = (float) (1.0 / std::sqrt((double) arg));
+    float y[64];
+    for (int d = 0; d < 64; ++d) y[d] = (v[d] * inv) * w[d];
+    for (int i = 0; i < 32; ++i) {
+        const float f = (float) std::pow(10000000.0, -(double) i / 32.0);
+        const float ang = (float) pos * f;
+        const float c = (float) std::cos((double) ang), s = (float) std::sin((double) ang);
+        const float x0 = y[i], x1 = y[i + 32];
+        out[i]      = x0 * c - x1 * s;
+        out[i + 32] = x0 * s + x1 * c;
+    }
+}
+
+// k_qk_norm_rope (kernels.cu:871-915): qf [32][64], kf [8][64] in place; K and
+// V rows (fp16) into kc / vc row pos ([pos][8][64]).
+void lko_qk_norm_rope(float * qf, float * kf, const float * vf, const float * qn, const float * kn,
+                      int pos, uint16_t * kc, uint16_t * vc) {
+    float out[64];
+    for (int h = 0; h < LKO_H; ++h) {
+        lko_norm_rope_row(qf + h * 64, qn, pos, out);
+        std::memcpy(qf + h * 64, out, sizeof out);
+    }
+    for (int h = 0; h < LKO_KV; ++h) {
+        lko_norm_rope_row(kf + h * 64, kn, pos, out);
+        std::memcpy(kf + h * 64, out, sizeof out);
+        const size_t off = ((size_t) pos * LKO_KV + h) * 64;
+        for (int d = 0; d < 64; ++d) {
+            kc[off + d] = lko_f2h(out[d]);
+            vc[off + d] = lko_f2h(vf[h * 64 + d]);
+        }
+    }
+}
+
+// k_pf_qknr (prefill.cu:975-1016): Y [m][3072] -> qh [m][2048] = fp16(q_rot *
+// 1/8), K/V rows P+t of kc / vc.
+void lko_pf_qknr(const float * Y, const float * qn, const float * kn, int m, int P,
+                 uint16_t * qh, uint16_t * kc, uint16_t * vc) {
+    float out[64];
+    for (int t = 0; t < m; ++t) {
+        const float * y = Y + (size_t) t * 3072;
+        for (int h = 0; h < LKO_H; ++h) {
+            lko_norm_rope_row(y + h * 64, qn, P + t, out);
+            for (int d = 0; d < 64; ++d) qh[(size_t) t * 2048 + h * 64 + d] = lko_f2h(out[d] * 0.125f);
+        }
+        for (int h = 0; h < LKO_KV; ++h) {
+            lko_norm_rope_row(y + 2048 + h * 64, kn, P + t, out);
+            const size_t off = ((size_t) (P + t) * LKO_KV + h) * 64;
+            for (int d = 0; d < 64; ++d) {
+                kc[off + d] = lko_f2h(out[d]);
+                vc[off + d] = lko_f2h(y[2560 + h * 64 + d]);
+            }
+        }
+    }
+}
+
 // max |a - b| / max |b| over n values (b is the reference).
 double lko_rel_err(const float * a, const double * b, size_t n) {
     double e = 0.0, r = 0.0;

@@ -49,6 +49,9 @@ def load():
         "lko_pf_ref": ([P, I, I, P, P, P, I, P], None),
         "lko_pf_ref8": ([P, P, P, P, I, I, P, P, I, P, P, I, I, P, I, P], None),
         "lko_qk_i32": ([P, I, P, I, P], None),
+        "lko_norm_rope_row": ([P, P, I, P], None),
+        "lko_qk_norm_rope": ([P, P, P, P, P, I, P, P], None),
+        "lko_pf_qknr": ([P, P, P, I, I, P, P, P], None),
         "lko_xs_fill_attn_case": ([P, S, P, P, P], None),
         "lko_sm_normal": ([U64, P, S], None),
         "lko_sm_uniform": ([U64, P, S, F, F], None),
@@ -191,6 +194,32 @@ def qk_i32(q8, m, k8, n) -> np.ndarray:
     s = np.empty((32, m, n), np.int32)
     load().lko_qk_i32(_p(q8), m, _p(k8), n, _p(s))
     return s
+
+
+# ---- attention-input producers (kernels.cu:871-915, prefill.cu:975-1016) ----------------
+def norm_rope_row(v, w, pos) -> np.ndarray:
+    v = np.ascontiguousarray(v, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty(64, np.float32)
+    load().lko_norm_rope_row(_p(v), _p(w), int(pos), _p(out))
+    return out
+
+
+def qk_norm_rope(qf, kf, vf, qn, kn, pos, kc, vc):
+    """In place on qf [32*64], kf [8*64] (fp32) and kc / vc (uint16 fp16 bits)."""
+    for a, t in ((qf, np.float32), (kf, np.float32), (kc, np.uint16), (vc, np.uint16)):
+        assert a.dtype == t and a.flags["C_CONTIGUOUS"]
+    vf, qn, kn = (np.ascontiguousarray(a, np.float32) for a in (vf, qn, kn))
+    load().lko_qk_norm_rope(_p(qf), _p(kf), _p(vf), _p(qn), _p(kn), int(pos), _p(kc), _p(vc))
+
+
+def pf_qknr(Y, qn, kn, m, P, kc, vc) -> np.ndarray:
+    """Returns qh (uint16 [m][2048]); writes rows P .. P+m-1 of kc / vc in place."""
+    Y, qn, kn = (np.ascontiguousarray(a, np.float32) for a in (Y, qn, kn))
+    assert kc.dtype == np.uint16 and vc.dtype == np.uint16
+    qh = np.zeros((m, 2048), np.uint16)
+    load().lko_pf_qknr(_p(Y), _p(qn), _p(kn), int(m), int(P), _p(qh), _p(kc), _p(vc))
+    return qh
 
 
 # ---- generators ---------------------------------------------------------------------

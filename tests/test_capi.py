@@ -55,6 +55,10 @@ def test_host_argument_errors():
     assert lib.lk_pf_attn8(p, p, p, p, 10, 0, p, p, 8, p, p, 0, 0, p, None) == 1   # kstride < P+m
     assert lib.lk_pf_qk_i32(p, 17, p, 16, p, None) == 1
     assert lib.lk_pf_kmean(p, 0, p, None) == 1
+    assert lib.lk_qk_norm_rope(None, p, p, p, p, p, p, p, None) == 1
+    assert lib.lk_pf_qknr(p, p, p, 4, 0, p, p, p, p, None, 8, None, None) == 1        # k8 without ksc
+    assert lib.lk_pf_qknr(p, p, p, 4, 0, p, p, p, p, p, 6, None, None) == 1          # kstride % 4
+    assert lib.lk_pf_qknr(None, None, None, 0, 0, None, None, None, None, None, 0, None, None) == 0
     assert lib.lk_pf_split_override(-2) == 1
     assert lib.lk_pf_split_override(0) == 0
     # empty work is a successful no-op

@@ -374,3 +374,80 @@ def test_rel_err_metric(oracle):
     a = np.array([1.0, 2.0, 3.5])
     b = np.array([1.0, 2.0, 4.0])
     assert oracle.rel_err(a, b) == pytest.approx(0.5 / 4.0)
+
+
+# ---- attention-input producers (kernels.cu:871-915, prefill.cu:975-1016) -------------------------
+def _textbook_norm_rope(v, w, pos):
+    """Independent float64 statement: RMS norm then NEOX rotation (first half
+    paired with second half), theta 1e7, eps 1e-5."""
+    v = v.astype(np.float64)
+    y = v / np.sqrt(np.mean(v * v) + 1e-5) * w.astype(np.float64)
+    i = np.arange(32, dtype=np.float64)
+    ang = pos * 10000000.0 ** (-i / 32.0)
+    c, s = np.cos(ang), np.sin(ang)
+    return np.concatenate([y[:32] * c - y[32:] * s, y[:32] * s + y[32:] * c])
+
+
+@pytest.mark.parametrize("pos", [0, 1, 7, 300])
+def test_norm_rope_row_matches_textbook(oracle, pos):
+    rng = np.random.default_rng(100 + pos)
+    for _ in range(20):
+        v = (rng.standard_normal(64) * rng.uniform(0.1, 30.0)).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+        got = oracle.norm_rope_row(v, w, pos).astype(np.float64)
+        want = _textbook_norm_rope(v, w, pos)
+        # fp32 rounding of the steps, plus the fp32 angle (pos * f rounded)
+        assert np.max(np.abs(got - want)) / np.max(np.abs(want)) <= 2e-6 + pos * 1.2e-7
+
+
+def test_norm_rope_row_position_zero_is_pure_norm(oracle):
+    rng = np.random.default_rng(7)
+    v = rng.standard_normal(64).astype(np.float32)
+    w = np.ones(64, np.float32)
+    got = oracle.norm_rope_row(v, w, 0)
+    y = v.astype(np.float64) / np.sqrt(np.mean(v.astype(np.float64) ** 2) + 1e-5)
+    assert np.max(np.abs(got - y)) <= 4e-7 * np.max(np.abs(y))
+    assert abs(np.mean(got.astype(np.float64) ** 2) - 1.0) < 1e-5 + 1e-5   # unit RMS (eps aside)
+
+
+def test_norm_rope_row_rotation_keeps_pair_norms(oracle):
+    # at a large position the angles are large, but each (i, i+32) pair is
+    # only rotated: its norm equals the norm-only pair
+    rng = np.random.default_rng(8)
+    v = rng.standard_normal(64).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+    y = oracle.norm_rope_row(v, w, 0).astype(np.float64)
+    r = oracle.norm_rope_row(v, w, 131071).astype(np.float64)
+    n0 = y[:32] ** 2 + y[32:] ** 2
+    n1 = r[:32] ** 2 + r[32:] ** 2
+    assert np.max(np.abs(n1 - n0) / n0) < 2e-6
+    # frequency 0 turns by exactly `pos` radians
+    assert abs(r[0] - (y[0] * math.cos(131071.0) - y[32] * math.sin(131071.0))) < 1e-5 * np.max(np.abs(y))
+
+
+def test_decode_and_prefill_producers_agree(oracle):
+    # the reference's own gate (test_prefill.cu:463-504): per token, decode's
+    # in-place q/k and cache rows equal the prefill kernel's outputs
+    rng = np.random.default_rng(9)
+    M, P = 6, 1000
+    S = P + M
+    Y = (rng.standard_normal((M, 3072)) * 3.0).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+    kn = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+    kc0 = np.zeros(S * 512, np.uint16)
+    vc0 = np.zeros(S * 512, np.uint16)
+    qh = oracle.pf_qknr(Y, qn, kn, M, P, kc0, vc0)
+    kc1 = np.zeros(S * 512, np.uint16)
+    vc1 = np.zeros(S * 512, np.uint16)
+    for t in range(M):
+        qf = Y[t, :2048].copy()
+        kf = Y[t, 2048:2560].copy()
+        vf = Y[t, 2560:].copy()
+        oracle.qk_norm_rope(qf, kf, vf, qn, kn, P + t, kc1, vc1)
+        assert np.array_equal(qh[t], (qf * np.float32(0.125)).astype(np.float16).view(np.uint16))
+        for h in range(8):
+            assert np.array_equal(kf[h * 64:(h + 1) * 64], oracle.norm_rope_row(Y[t, 2048 + h * 64:2048 + (h + 1) * 64], kn, P + t))
+    assert np.array_equal(kc0, kc1) and np.array_equal(vc0, vc1)
+    # V is copied unnormalised and unrotated; rows outside [P, P+M) untouched
+    assert np.array_equal(vc0.reshape(S, 8, 64)[P:], Y[:, 2560:].reshape(M, 8, 64).astype(np.float16).view(np.uint16))
+    assert not kc0.reshape(S, 512)[:P].any()
