@@ -111,6 +111,47 @@ def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters):
     return res
 
 
+def bench_decode_step(lk, steps, warmup, layers=10, ctx=32768):
+    """The decode step graph (per layer: stage q/k, qk norm + RoPE + cache
+    append, split, combine; then d_pos += 1; reference engine.cu:1328-1342,
+    1750-1760) replayed `steps` times around a 32k context: the attention slice
+    of a whole decode step, producers included."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(91)
+    Ls = []
+    for _ in range(layers):
+        Ls.append({"q_src": torch.randn(2048, device="cuda", generator=g),
+                   "k_src": torch.randn(512, device="cuda", generator=g),
+                   "v_src": torch.randn(512, device="cuda", generator=g),
+                   "q": torch.empty(2048, device="cuda"), "k": torch.empty(512, device="cuda"),
+                   "q_norm": torch.rand(64, device="cuda", generator=g) + 0.5,
+                   "k_norm": torch.rand(64, device="cuda", generator=g) + 0.5,
+                   "kc": torch.randn(ctx, 8, 64, device="cuda", generator=g).half(),
+                   "vc": torch.randn(ctx, 8, 64, device="cuda", generator=g).half(),
+                   "out": torch.empty(32, 64, device="cuda")})
+    start = ctx - steps - warmup
+    d_pos = torch.tensor([start], dtype=torch.int32, device="cuda")
+    part = torch.empty(lk.part_bytes() // 4, device="cuda")
+    gr = lk.DecodeStepGraph(Ls, d_pos, part)
+    st = gr.stream
+    torch.cuda.synchronize()
+    gr.run(warmup)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    gr.run(steps)
+    e1.record(st)
+    st.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    assert int(d_pos.item()) == ctx
+    nodes = gr.nodes()
+    gr.close()
+    del Ls
+    torch.cuda.empty_cache()
+    return {"layers": layers, "context": f"{start + warmup} .. {ctx - 1}", "steps": steps,
+            "us_per_step": ms * 1e3, "us_per_layer": ms * 1e3 / layers, "graph_nodes": nodes}
+
+
 def pf_ops(m, P):
     """Algorithmic ops of one causal chunk: per (query, key) pair 64 int8 MAC for
     Q.K and 64 fp16 MAC for P.V, 2 ops per MAC (test_prefill.cu:652)."""
@@ -390,6 +431,9 @@ def main():
     c3 = bench_decode(lk, lkc, "C3", max(20, args.steps // 4), max(3, args.warmup // 4), args.kernel_iters // 2)
     log(json.dumps(c3))
     results = {"C2_decode_32k": c2, "C3_decode_131k": c3}
+    log("decode step graph (producers + attention, 10 layers, 32k context)")
+    results["C2_decode_step_graph"] = bench_decode_step(lk, 50, 10)
+    log(json.dumps(results["C2_decode_step_graph"]))
     if not args.skip_prefill:
         log("prefill C4 (4096 chunk, P=0)")
         results["C4_prefill_4k"] = bench_prefill_c4(lk, lkc, 20)

@@ -111,6 +111,35 @@ int lk_decode_graph_launch(lk_decode_graph * graph, void * stream);
 int lk_decode_graph_nodes(const lk_decode_graph * graph, size_t * n_nodes);
 int lk_decode_graph_destroy(lk_decode_graph * graph);
 
+/* ---- decode step graph -----------------------------------------------------
+ * The engine captures its whole position-independent decode step once and
+ * replays it, the last kernel advancing d_pos on the device (reference
+ * engine.cu:1328-1342 capture, 1750-1760 replay loop, kernels.cu:994 advance).
+ * This is that step's attention slice: per layer, the q/k/v projection rows
+ * (q_src, k_src, v_src fp32, standing in for the projection GEMV's output; they
+ * are copied into the working q / k buffers), lk_qk_norm_rope (K/V appended
+ * at row *d_pos of the layer's cache), split and combine; then *d_pos += 1.
+ * Replaying it n times runs n decode steps with no host work in between.
+ * All pointers are device pointers owned by the caller; `part` is shared by
+ * the layers. */
+typedef struct lk_decode_layer {
+    const float * q_src;            /* fp32 [32][64] */
+    const float * k_src;            /* fp32 [8][64] */
+    const float * v_src;            /* fp32 [8][64] */
+    float *       q;                /* fp32 [32][64] working q (normalised + rotated) */
+    float *       k;                /* fp32 [8][64] working k */
+    const float * q_norm;           /* fp32 [64] */
+    const float * k_norm;           /* fp32 [64] */
+    void *        kc;               /* fp16 [max_seq][8][64] */
+    void *        vc;               /* fp16 [max_seq][8][64] */
+    float *       out;              /* fp32 [32][64] or NULL */
+    lk_block_q8_1 * yq8;            /* [64] or NULL */
+} lk_decode_layer;
+int lk_decode_step_graph_create(int n_layers, const lk_decode_layer * layers, int * d_pos,
+                                float * part, void * stream, lk_decode_graph ** graph);
+/* Replays a graph n_steps times on `stream` (no synchronisation). */
+int lk_decode_graph_run(lk_decode_graph * graph, int n_steps, void * stream);
+
 /* ---- prefill: int8 quantisers ---------------------------------------------
  * Per (row, head) 64-wide absmax quantisation (reference prefill.cu:1255-1267):
  * d = amax/127, q = rint(v * (127/amax)), scale = d * mul.  Bit-exact. */

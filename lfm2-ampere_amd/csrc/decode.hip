@@ -512,6 +512,76 @@ extern "C" int lk_decode_graph_create(int n_layers, const float * const * q,
     return 0;
 }
 
+// Stand-in for the projection GEMV's output write: the layer's q and k rows
+// into the working buffers (in place of the engine's qv / kv).
+__global__ void __launch_bounds__(256) lk_k_stage_qk(const float * __restrict__ qs, const float * __restrict__ ks,
+                                                     float * __restrict__ q, float * __restrict__ k) {
+    const int t = threadIdx.x;                        // 256 threads x 8 + 2 floats
+    *(lk_f4 *) (q + 8 * t)     = *(const lk_f4 *) (qs + 8 * t);
+    *(lk_f4 *) (q + 8 * t + 4) = *(const lk_f4 *) (qs + 8 * t + 4);
+    if (t < 128) *(lk_f4 *) (k + 4 * t) = *(const lk_f4 *) (ks + 4 * t);
+}
+// The step's last node: the position advance (reference kernels.cu:994).
+__global__ void lk_k_advance_pos(int * __restrict__ d_pos) {
+    if (threadIdx.x == 0) *d_pos = *d_pos + 1;
+}
+
+extern "C" int lk_decode_step_graph_create(int n_layers, const lk_decode_layer * layers, int * d_pos,
+                                           float * part, void * stream, lk_decode_graph ** graph) {
+    if (!graph) return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: graph is null");
+    *graph = nullptr;
+    if (n_layers <= 0 || !layers || !d_pos || !part)
+        return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: bad arguments");
+    if (!stream)
+        return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: capture needs a non-default stream");
+    for (int i = 0; i < n_layers; ++i) {
+        const lk_decode_layer & L = layers[i];
+        if (!L.q_src || !L.k_src || !L.v_src || !L.q || !L.k || !L.q_norm || !L.k_norm || !L.kc || !L.vc)
+            return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: null pointer for layer %d", i);
+    }
+    hipStream_t st = lk_stream(stream);
+    hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return lk_fail((int) e, "hipStreamBeginCapture: %s", hipGetErrorString(e));
+    int rc = 0;
+    for (int i = 0; i < n_layers && !rc; ++i) {
+        const lk_decode_layer & L = layers[i];
+        hipLaunchKernelGGL(lk_k_stage_qk, dim3(1), dim3(256), 0, st, L.q_src, L.k_src, L.q, L.k);
+        rc = lk_launch_status("lk_decode_step_graph_create");
+        if (!rc) rc = lk_qknr_decode_launch(L.q, L.k, L.v_src, L.q_norm, L.k_norm, d_pos, L.kc, L.vc, st);
+        if (!rc) rc = lk_split_launch(L.q, L.kc, L.vc, d_pos, part, st);
+        if (!rc) rc = lk_combine_launch(part, d_pos, L.out, L.yq8, st);
+    }
+    if (!rc) {
+        hipLaunchKernelGGL(lk_k_advance_pos, dim3(1), dim3(64), 0, st, d_pos);
+        rc = lk_launch_status("lk_decode_step_graph_create");
+    }
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(st, &g);
+    if (rc) { if (g) (void) hipGraphDestroy(g); return rc; }
+    if (e != hipSuccess) return lk_fail((int) e, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    lk_decode_graph * G = new lk_decode_graph;
+    G->graph = g;
+    e = hipGraphInstantiate(&G->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void) hipGraphDestroy(g);
+        delete G;
+        return lk_fail((int) e, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    (void) hipGraphGetNodes(g, nullptr, &G->nodes);
+    *graph = G;
+    return 0;
+}
+
+extern "C" int lk_decode_graph_run(lk_decode_graph * graph, int n_steps, void * stream) {
+    if (!graph || !graph->exec || n_steps < 0)
+        return lk_fail(hipErrorInvalidValue, "lk_decode_graph_run: bad arguments");
+    for (int i = 0; i < n_steps; ++i) {
+        const hipError_t e = hipGraphLaunch(graph->exec, lk_stream(stream));
+        if (e != hipSuccess) return lk_fail((int) e, "hipGraphLaunch (step %d): %s", i, hipGetErrorString(e));
+    }
+    return 0;
+}
+
 extern "C" int lk_decode_graph_launch(lk_decode_graph * graph, void * stream) {
     if (!graph || !graph->exec) return lk_fail(hipErrorInvalidValue, "lk_decode_graph_launch: no graph");
     const hipError_t e = hipGraphLaunch(graph->exec, lk_stream(stream));

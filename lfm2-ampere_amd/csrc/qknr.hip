@@ -165,14 +165,19 @@ lk_k_pf_qknr(const float * __restrict__ Y, const float * __restrict__ qn, const 
 
 // ---------------------------------------------------------------------------
 // C ABI
+int lk_qknr_decode_launch(float * qf, float * kf, const float * vf, const float * qn, const float * kn,
+                          const int * d_pos, void * kc, void * vc, hipStream_t st) {
+    hipLaunchKernelGGL(lk_k_qk_norm_rope, dim3(1), dim3(LK_QKNR_THREADS), 0, st,
+                       qf, kf, vf, qn, kn, d_pos, (_Float16 *) kc, (_Float16 *) vc);
+    return lk_launch_status("lk_qk_norm_rope");
+}
+
 extern "C" int lk_qk_norm_rope(float * qf, float * kf, const float * vf, const float * qn,
                                const float * kn, const int * d_pos, void * kc, void * vc,
                                void * stream) {
     if (!qf || !kf || !vf || !qn || !kn || !d_pos || !kc || !vc)
         return lk_fail(hipErrorInvalidValue, "lk_qk_norm_rope: null pointer argument");
-    hipLaunchKernelGGL(lk_k_qk_norm_rope, dim3(1), dim3(LK_QKNR_THREADS), 0, lk_stream(stream),
-                       qf, kf, vf, qn, kn, d_pos, (_Float16 *) kc, (_Float16 *) vc);
-    return lk_launch_status("lk_qk_norm_rope");
+    return lk_qknr_decode_launch(qf, kf, vf, qn, kn, d_pos, kc, vc, lk_stream(stream));
 }
 
 extern "C" int lk_pf_qknr(const float * Y, const float * qn, const float * kn, int m, int P,

@@ -30,6 +30,7 @@ EXPORTS = (
     "lk_decode_graph_destroy",
     "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_split_override",
     "lk_pf_qk_i32", "lk_qk_norm_rope", "lk_pf_qknr",
+    "lk_decode_step_graph_create", "lk_decode_graph_run",
 )
 
 
@@ -72,6 +73,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_qk_i32": ([P, I, P, I, P, P], I),
         "lk_qk_norm_rope": ([P, P, P, P, P, P, P, P, P], I),
         "lk_pf_qknr": ([P, P, P, I, I, P, P, P, P, P, I, P, P], I),
+        "lk_decode_step_graph_create": ([I, P, P, P, P, P], I),
+        "lk_decode_graph_run": ([P, I, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -142,6 +145,56 @@ def attn_decode(q, kc, vc, d_pos, part, out=None, yq8=None, stream=None) -> None
 def attention_decode(q, kc, vc, d_pos, out=None, yq8=None, stream=None) -> None:
     _check(load().lk_attention_decode(_ptr(q), _ptr(kc), _ptr(vc), _ptr(d_pos), _ptr(out),
                                       _ptr(yq8), _stream(stream)), "lk_attention_decode")
+
+
+class DecodeLayer(ctypes.Structure):
+    """lk_decode_layer (include/lk_attn.h): one layer's buffers for the step graph."""
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("q_src", "k_src", "v_src", "q", "k", "q_norm", "k_norm", "kc", "vc", "out", "yq8")]
+
+
+class DecodeStepGraph:
+    """The decode step's attention slice (per layer: stage q/k, qk norm + RoPE +
+    cache append, split, combine; then d_pos += 1) captured into one hipGraph;
+    run(n) replays it n times."""
+
+    def __init__(self, layers: Sequence[dict], d_pos, part, stream=None):
+        import torch
+        n = len(layers)
+        arr = (DecodeLayer * n)()
+        for i, L in enumerate(layers):
+            for f, _ in DecodeLayer._fields_:
+                setattr(arr[i], f, _ptr(L.get(f)))
+        self._keep = (layers, d_pos, part, arr)
+        self._stream = stream if stream is not None else torch.cuda.Stream()
+        h = ctypes.c_void_p()
+        _check(load().lk_decode_step_graph_create(n, arr, _ptr(d_pos), _ptr(part),
+                                                  self._stream.cuda_stream, ctypes.byref(h)),
+               "lk_decode_step_graph_create")
+        self._h = h
+
+    @property
+    def stream(self):
+        return self._stream
+
+    def nodes(self) -> int:
+        n = ctypes.c_size_t()
+        _check(load().lk_decode_graph_nodes(self._h, ctypes.byref(n)), "lk_decode_graph_nodes")
+        return n.value
+
+    def run(self, n_steps: int = 1) -> None:
+        _check(load().lk_decode_graph_run(self._h, int(n_steps), self._stream.cuda_stream), "lk_decode_graph_run")
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().lk_decode_graph_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class DecodeGraph:

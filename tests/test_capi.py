@@ -69,6 +69,8 @@ def test_host_argument_errors():
     assert lib.lk_decode_graph_create(0, None, None, None, None, None, None, None, p, ctypes.byref(h)) == 1
     assert lib.lk_decode_graph_launch(None, None) == 1
     assert lib.lk_decode_graph_destroy(None) == 0
+    assert lib.lk_decode_step_graph_create(0, None, p, p, p, ctypes.byref(h)) == 1
+    assert lib.lk_decode_graph_run(None, 1, None) == 1
 
 
 def test_python_mirror_fails_loudly_without_library(tmp_path):

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import abs_err, d_pos_for, dev, dev_h, host, note
+from gpu_util import abs_err, d_pos_for, dev, dev_h, host, note, host_h
 
 pytestmark = pytest.mark.gpu
 
@@ -209,3 +209,68 @@ def test_config_c2(lk, oracle):
 
 def test_config_c3_graph(lk, oracle):
     _check_config(lk, oracle, "C3", 10, [0, 9])
+
+
+def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
+    """The decode step graph (per layer: stage, qk norm + RoPE + cache append,
+    split, combine; then d_pos += 1) replayed n times = n decode steps: cache
+    rows, d_pos and every layer's output against the oracle, and the replay
+    bit-identical to the same kernels called eagerly."""
+    rng = np.random.default_rng(61)
+    layers, P0, steps, cap = 3, 1000, 5, 1024
+    note(f"decode step graph: {layers} layers, {steps} steps from position {P0}")
+    Ls, host_in = [], []
+    for i in range(layers):
+        qs = (rng.standard_normal(2048) * 2).astype(np.float32)
+        ks = (rng.standard_normal(512) * 2).astype(np.float32)
+        vs = rng.standard_normal(512).astype(np.float32)
+        qn = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+        kn = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+        kc0 = np.zeros((cap, 8, 64), np.uint16)
+        vc0 = np.zeros((cap, 8, 64), np.uint16)
+        kc0[:P0] = rng.standard_normal((P0, 8, 64)).astype(np.float16).view(np.uint16)
+        vc0[:P0] = rng.standard_normal((P0, 8, 64)).astype(np.float16).view(np.uint16)
+        host_in.append((qs, ks, vs, qn, kn, kc0, vc0))
+        Ls.append({"q_src": dev(qs), "k_src": dev(ks), "v_src": dev(vs),
+                   "q": torch.empty(2048, device="cuda"), "k": torch.empty(512, device="cuda"),
+                   "q_norm": dev(qn), "k_norm": dev(kn), "kc": dev_h(kc0), "vc": dev_h(vc0),
+                   "out": torch.full((32, 64), float("nan"), device="cuda"),
+                   "yq8": torch.zeros(64 * 36, dtype=torch.uint8, device="cuda")})
+    d_pos = torch.tensor([P0], dtype=torch.int32, device="cuda")
+    part = torch.empty(lk.part_bytes() // 4, device="cuda")
+    g = lk.DecodeStepGraph(Ls, d_pos, part)
+    assert g.nodes() == 4 * layers + 1
+    g.run(steps)
+    g.stream.synchronize()
+    assert int(d_pos.item()) == P0 + steps
+    # eager replay of the same kernels on fresh copies must match bit for bit
+    E = [{k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in L.items()} for L in Ls]
+    for i, (qs, ks, vs, qn, kn, kc0, vc0) in enumerate(host_in):
+        E[i]["kc"], E[i]["vc"] = dev_h(kc0), dev_h(vc0)
+    dp = torch.tensor([P0], dtype=torch.int32, device="cuda")
+    for s in range(steps):
+        for L in E:
+            L["q"].copy_(L["q_src"]); L["k"].copy_(L["k_src"])
+            lk.qk_norm_rope(L["q"], L["k"], L["v_src"], L["q_norm"], L["k_norm"], dp, L["kc"], L["vc"])
+            lk.attn_split(L["q"], L["kc"], L["vc"], dp, part)
+            lk.attn_combine(part, dp, L["out"], L["yq8"])
+        dp += 1
+    torch.cuda.synchronize()
+    for L, M in zip(Ls, E):
+        assert torch.equal(L["out"].view(torch.int32), M["out"].view(torch.int32))
+        assert torch.equal(L["yq8"], M["yq8"])
+        assert torch.equal(L["kc"].view(torch.int16), M["kc"].view(torch.int16))
+    # against the oracle: appended rows and the last step's output
+    last = P0 + steps - 1
+    for (qs, ks, vs, qn, kn, kc0, vc0), L in zip(host_in, Ls):
+        kc_h = host_h(L["kc"]).reshape(cap, 8, 64)
+        vc_h = host_h(L["vc"]).reshape(cap, 8, 64)
+        assert np.array_equal(kc_h[:P0], kc0[:P0]) and np.array_equal(vc_h[:P0], vc0[:P0])
+        for s in range(steps):
+            krow = np.concatenate([oracle.norm_rope_row(ks[h * 64:(h + 1) * 64], kn, P0 + s) for h in range(8)])
+            assert np.array_equal(kc_h[P0 + s].reshape(-1), krow.astype(np.float16).view(np.uint16))
+            assert np.array_equal(vc_h[P0 + s].reshape(-1), vs.astype(np.float16).view(np.uint16))
+        q_rot = np.concatenate([oracle.norm_rope_row(qs[h * 64:(h + 1) * 64], qn, last) for h in range(32)])
+        ref = oracle.decode_ref(q_rot.reshape(32, 64), kc_h[:last + 1].reshape(-1), vc_h[:last + 1].reshape(-1), last + 1)
+        assert oracle.rel_err(host(L["out"]), ref) <= 2e-3
+    g.close()
