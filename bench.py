@@ -112,8 +112,8 @@ def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters):
 
 
 def bench_decode_step(lk, steps, warmup, layers=10, ctx=32768):
-    """The decode step graph (per layer: stage q/k, qk norm + RoPE + cache
-    append, split, combine; then d_pos += 1; reference engine.cu:1328-1342,
+    """The decode step graph (per layer: qk norm + RoPE + cache append, split,
+    combine; then d_pos += 1; reference engine.cu:1328-1342,
     1750-1760) replayed `steps` times around a 32k context: the attention slice
     of a whole decode step, producers included."""
     import torch
@@ -289,6 +289,45 @@ def bench_producers(lk, iters):
     }
 
 
+def bench_pf_driver(lk, n_tok=32768, chunks=(4096, 8192)):
+    """The prefill chunk driver (engine.cu:1064-1124, 1255-1260) over an
+    n_tok prompt for one attention layer, per chunk size (the engine's default
+    is 8192, engine.cu:1315): producers + int8 K + Q quantiser + attention,
+    synthetic projections."""
+    import torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(93)
+    qn = torch.rand(64, device="cuda", generator=g) + 0.5
+    kn = torch.rand(64, device="cuda", generator=g) + 0.5
+    kc = torch.empty(n_tok, 8, 64, dtype=torch.float16, device="cuda")
+    vc = torch.empty_like(kc)
+    res = {}
+    for mc in chunks:
+        ctx = lk.PrefillCtx(1, mc, n_tok)
+        Y = torch.randn(mc, 3072, device="cuda", generator=g) * 3.0
+        o = torch.empty(mc, 2048, device="cuda")
+        st = torch.cuda.Stream()
+
+        def prompt():
+            for p0 in range(0, n_tok, mc):
+                ctx.chunk_attn(0, Y, qn, kn, mc, p0, kc, vc, o, stream=st)
+                ctx.chunk_done(p0 + mc)
+        prompt()                                      # warm-up
+        st.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        prompt()
+        e1.record(st)
+        st.synchronize()
+        ms = e0.elapsed_time(e1)
+        res[f"chunk_{mc}"] = {"ms": ms, "tokens_per_s": n_tok / (ms * 1e-3)}
+        ctx.close()
+        del Y, o
+    del kc, vc
+    torch.cuda.empty_cache()
+    return {"prompt_tokens": n_tok, "layers": 1, **res}
+
+
 def cpu_baseline(seconds, prefill=True):
     """The reference's CPU path restated in the oracle (float64, single
     thread): decode attention (tests/test_attn.cu:46-74) on a full C2 layer and
@@ -431,7 +470,7 @@ def main():
     c3 = bench_decode(lk, lkc, "C3", max(20, args.steps // 4), max(3, args.warmup // 4), args.kernel_iters // 2)
     log(json.dumps(c3))
     results = {"C2_decode_32k": c2, "C3_decode_131k": c3}
-    log("decode step graph (producers + attention, 10 layers, 32k context)")
+    log("decode step graph (producer + attention, 10 layers, 32k context)")
     results["C2_decode_step_graph"] = bench_decode_step(lk, 50, 10)
     log(json.dumps(results["C2_decode_step_graph"]))
     if not args.skip_prefill:
@@ -444,6 +483,9 @@ def main():
         log("attention-input producers (qk norm + rope + cache write)")
         results["producers"] = bench_producers(lk, 20)
         log(json.dumps(results["producers"]))
+        log("prefill chunk driver (32k prompt, one attention layer)")
+        results["prefill_driver_32k"] = bench_pf_driver(lk)
+        log(json.dumps(results["prefill_driver_32k"]))
 
     cpu = None
     if not args.skip_cpu:

@@ -115,10 +115,11 @@ int lk_decode_graph_destroy(lk_decode_graph * graph);
  * The engine captures its whole position-independent decode step once and
  * replays it, the last kernel advancing d_pos on the device (reference
  * engine.cu:1328-1342 capture, 1750-1760 replay loop, kernels.cu:994 advance).
- * This is that step's attention slice: per layer, the q/k/v projection rows
- * (q_src, k_src, v_src fp32, standing in for the projection GEMV's output; they
- * are copied into the working q / k buffers), lk_qk_norm_rope (K/V appended
- * at row *d_pos of the layer's cache), split and combine; then *d_pos += 1.
+ * This is that step's attention slice: per layer, the q/k norm + RoPE of the
+ * q/k/v projection rows (q_src, k_src, v_src fp32, the projection GEMV's
+ * output) into the working q / k buffers with K/V appended at row *d_pos of the
+ * layer's cache (lk_qk_norm_rope's arithmetic, out of place), split and
+ * combine; then *d_pos += 1.
  * Replaying it n times runs n decode steps with no host work in between.
  * All pointers are device pointers owned by the caller; `part` is shared by
  * the layers. */
@@ -221,6 +222,31 @@ int lk_qk_norm_rope(float * qf, float * kf, const float * vf, const float * qn,
 int lk_pf_qknr(const float * Y, const float * qn, const float * kn, int m, int P,
                void * qh, void * kc, void * vc, int8_t * k8, float * ksc, int kstride,
                const float * cm, void * stream);
+
+/* ---- prefill chunk driver ---------------------------------------------------
+ * The attention slice of the engine's prefill chunk (reference engine.cu:1064-
+ * 1124 in pf_chunk, state engine.cu:236-256): per attention layer and chunk of
+ * m tokens at [pos0, pos0+m): producers (+ the new rows' int8 K), the int8 K
+ * copy caught up over [k8_valid, pos0) (keys decode steps appended since the
+ * last prefill), the smoothing mean re-derived on a new context (pos0 == 0)
+ * when ksmooth, the Q quantiser and the int8 (attn8 != 0) or fp16 attention
+ * into o fp32 [m][2048].  lk_pf_chunk_done(pos0 + m) after the chunk's last
+ * layer sets k8_valid (engine.cu:1251).  create allocates the chunk buffers
+ * and, per layer, the int8 K copy [max_seq][8][64], its scales and the mean
+ * (engine.cu:974-985); nothing is allocated per call.  The chunking of a
+ * prompt is the caller's loop (engine.cu:1255-1260; chunk 8192 by default,
+ * engine.cu:1315). */
+typedef struct lk_pf_ctx lk_pf_ctx;
+int lk_pf_ctx_create(int n_layers, int max_chunk, int max_seq, int attn8, int ksmooth,
+                     int near, int sink, lk_pf_ctx ** ctx);
+int lk_pf_ctx_destroy(lk_pf_ctx * ctx);
+int lk_pf_chunk_attn(lk_pf_ctx * ctx, int layer, const float * Y, const float * qn,
+                     const float * kn, int m, int pos0, void * kc, void * vc, float * o,
+                     void * stream);
+int lk_pf_chunk_done(lk_pf_ctx * ctx, int pos_end);
+/* The context's device buffers for one layer (any output may be NULL). */
+int lk_pf_ctx_buffers(const lk_pf_ctx * ctx, int layer, void ** qh, int8_t ** k8,
+                      float ** ksc, float ** cm, int * kstride, int * k8_valid);
 
 /* ---- test hook --------------------------------------------------------------
  * The raw int32 Q.K^T sums of the int8 scoring path, computed by the same

@@ -512,15 +512,6 @@ extern "C" int lk_decode_graph_create(int n_layers, const float * const * q,
     return 0;
 }
 
-// Stand-in for the projection GEMV's output write: the layer's q and k rows
-// into the working buffers (in place of the engine's qv / kv).
-__global__ void __launch_bounds__(256) lk_k_stage_qk(const float * __restrict__ qs, const float * __restrict__ ks,
-                                                     float * __restrict__ q, float * __restrict__ k) {
-    const int t = threadIdx.x;                        // 256 threads x 8 + 2 floats
-    *(lk_f4 *) (q + 8 * t)     = *(const lk_f4 *) (qs + 8 * t);
-    *(lk_f4 *) (q + 8 * t + 4) = *(const lk_f4 *) (qs + 8 * t + 4);
-    if (t < 128) *(lk_f4 *) (k + 4 * t) = *(const lk_f4 *) (ks + 4 * t);
-}
 // The step's last node: the position advance (reference kernels.cu:994).
 __global__ void lk_k_advance_pos(int * __restrict__ d_pos) {
     if (threadIdx.x == 0) *d_pos = *d_pos + 1;
@@ -545,9 +536,10 @@ extern "C" int lk_decode_step_graph_create(int n_layers, const lk_decode_layer *
     int rc = 0;
     for (int i = 0; i < n_layers && !rc; ++i) {
         const lk_decode_layer & L = layers[i];
-        hipLaunchKernelGGL(lk_k_stage_qk, dim3(1), dim3(256), 0, st, L.q_src, L.k_src, L.q, L.k);
-        rc = lk_launch_status("lk_decode_step_graph_create");
-        if (!rc) rc = lk_qknr_decode_launch(L.q, L.k, L.v_src, L.q_norm, L.k_norm, d_pos, L.kc, L.vc, st);
+        // the producer reads the projection rows and writes the working q / k
+        // (the in-place API's arithmetic, out of place)
+        rc = lk_qknr_decode_launch(L.q_src, L.k_src, L.q, L.k, L.v_src, L.q_norm, L.k_norm, d_pos,
+                                   L.kc, L.vc, st);
         if (!rc) rc = lk_split_launch(L.q, L.kc, L.vc, d_pos, part, st);
         if (!rc) rc = lk_combine_launch(part, d_pos, L.out, L.yq8, st);
     }

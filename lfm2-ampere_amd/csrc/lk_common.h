@@ -199,8 +199,10 @@ __device__ __forceinline__ void lk_wait_vm() {
 }
 
 // ---- launchers shared between translation units -------------------------------
-int lk_qknr_decode_launch(float * qf, float * kf, const float * vf, const float * qn, const float * kn,
-                          const int * d_pos, void * kc, void * vc, hipStream_t st);
+// qs/ks -> qf/kf (may alias: in place)
+int lk_qknr_decode_launch(const float * qs, const float * ks, float * qf, float * kf, const float * vf,
+                          const float * qn, const float * kn, const int * d_pos, void * kc, void * vc,
+                          hipStream_t st);
 
 // ---- host-side error plumbing (lk_host.cpp) -----------------------------------
 int lk_fail(int code, const char * fmt, ...);

@@ -95,10 +95,11 @@ __device__ __forceinline__ void lk_load8f(const float * __restrict__ src, float 
     for (int i = 0; i < 4; ++i) { v[i] = a[i]; v[4 + i] = b[i]; }
 }
 
-// Decode: one token at position *d_pos; qf [32][64] and kf [8][64] fp32 are
-// normalised and rotated in place, K and V rows go to the fp16 caches.
+// Decode: one token at position *d_pos.  q and k rows are read from qs / ks
+// (fp32 [32][64] / [8][64]) and written, normalised and rotated, to qf / kf
+// (the same buffers for the in-place API); K and V rows go to the fp16 caches.
 __global__ void __launch_bounds__(LK_QKNR_THREADS)
-lk_k_qk_norm_rope(float * __restrict__ qf, float * __restrict__ kf, const float * __restrict__ vf,
+lk_k_qk_norm_rope(const float * qs, const float * ks, float * qf, float * kf, const float * __restrict__ vf,
                   const float * __restrict__ qn, const float * __restrict__ kn,
                   const int * __restrict__ d_pos, _Float16 * __restrict__ kc, _Float16 * __restrict__ vc) {
     __shared__ float s_c[LK_HEAD_DIM / 2], s_s[LK_HEAD_DIM / 2];
@@ -108,9 +109,10 @@ lk_k_qk_norm_rope(float * __restrict__ qf, float * __restrict__ kf, const float 
     const int g = threadIdx.x >> 3, j = threadIdx.x & 7;
     const bool isq = g < LK_N_HEADS;
     const int h = isq ? g : g - LK_N_HEADS;
+    const float * src = isq ? qs + h * LK_HEAD_DIM : ks + h * LK_HEAD_DIM;
     float * row = isq ? qf + h * LK_HEAD_DIM : kf + h * LK_HEAD_DIM;
     float v[8], out[8];
-    lk_load8f(row + 8 * j, v);
+    lk_load8f(src + 8 * j, v);
     lk_norm_rope8(v, isq ? qn : kn, s_c, s_s, j, out);
     *(lk_f4 *) (row + 8 * j)     = (lk_f4){ out[0], out[1], out[2], out[3] };
     *(lk_f4 *) (row + 8 * j + 4) = (lk_f4){ out[4], out[5], out[6], out[7] };
@@ -165,10 +167,11 @@ lk_k_pf_qknr(const float * __restrict__ Y, const float * __restrict__ qn, const 
 
 // ---------------------------------------------------------------------------
 // C ABI
-int lk_qknr_decode_launch(float * qf, float * kf, const float * vf, const float * qn, const float * kn,
-                          const int * d_pos, void * kc, void * vc, hipStream_t st) {
+int lk_qknr_decode_launch(const float * qs, const float * ks, float * qf, float * kf, const float * vf,
+                          const float * qn, const float * kn, const int * d_pos, void * kc, void * vc,
+                          hipStream_t st) {
     hipLaunchKernelGGL(lk_k_qk_norm_rope, dim3(1), dim3(LK_QKNR_THREADS), 0, st,
-                       qf, kf, vf, qn, kn, d_pos, (_Float16 *) kc, (_Float16 *) vc);
+                       qs, ks, qf, kf, vf, qn, kn, d_pos, (_Float16 *) kc, (_Float16 *) vc);
     return lk_launch_status("lk_qk_norm_rope");
 }
 
@@ -177,7 +180,7 @@ extern "C" int lk_qk_norm_rope(float * qf, float * kf, const float * vf, const f
                                void * stream) {
     if (!qf || !kf || !vf || !qn || !kn || !d_pos || !kc || !vc)
         return lk_fail(hipErrorInvalidValue, "lk_qk_norm_rope: null pointer argument");
-    return lk_qknr_decode_launch(qf, kf, vf, qn, kn, d_pos, kc, vc, lk_stream(stream));
+    return lk_qknr_decode_launch(qf, kf, qf, kf, vf, qn, kn, d_pos, kc, vc, lk_stream(stream));
 }
 
 extern "C" int lk_pf_qknr(const float * Y, const float * qn, const float * kn, int m, int P,

@@ -31,6 +31,7 @@ EXPORTS = (
     "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_split_override",
     "lk_pf_qk_i32", "lk_qk_norm_rope", "lk_pf_qknr",
     "lk_decode_step_graph_create", "lk_decode_graph_run",
+    "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
 )
 
 
@@ -50,6 +51,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         raise FileNotFoundError(
             f"{path} is missing: build it with `make -C lfm2-ampere_amd` "
             "(or __graft_entry__.build()); there is no fallback path")
+    # torch (whose tensors this module passes as device memory) carries its own
+    # HIP runtime under the same soname; load it first so the process has one
+    # runtime and torch's streams and allocations are valid for the library.
+    import torch  # noqa: F401
     lib = ctypes.CDLL(path)
     P, I, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
     sig = {
@@ -75,6 +80,11 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_qknr": ([P, P, P, I, I, P, P, P, P, P, I, P, P], I),
         "lk_decode_step_graph_create": ([I, P, P, P, P, P], I),
         "lk_decode_graph_run": ([P, I, P], I),
+        "lk_pf_ctx_create": ([I, I, I, I, I, I, I, P], I),
+        "lk_pf_ctx_destroy": ([P], I),
+        "lk_pf_chunk_attn": ([P, I, P, P, P, I, I, P, P, P, P], I),
+        "lk_pf_chunk_done": ([P, I], I),
+        "lk_pf_ctx_buffers": ([P, I, P, P, P, P, P, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -154,9 +164,9 @@ class DecodeLayer(ctypes.Structure):
 
 
 class DecodeStepGraph:
-    """The decode step's attention slice (per layer: stage q/k, qk norm + RoPE +
-    cache append, split, combine; then d_pos += 1) captured into one hipGraph;
-    run(n) replays it n times."""
+    """The decode step's attention slice (per layer: qk norm + RoPE of the
+    projection rows + cache append, split, combine; then d_pos += 1) captured
+    into one hipGraph; run(n) replays it n times."""
 
     def __init__(self, layers: Sequence[dict], d_pos, part, stream=None):
         import torch
@@ -290,3 +300,41 @@ def qk_norm_rope(qf, kf, vf, qn, kn, d_pos, kc, vc, stream=None) -> None:
 def pf_qknr(Y, qn, kn, m, P, qh, kc, vc, k8=None, ksc=None, kstride=0, cm=None, stream=None) -> None:
     _check(load().lk_pf_qknr(_ptr(Y), _ptr(qn), _ptr(kn), int(m), int(P), _ptr(qh), _ptr(kc), _ptr(vc),
                              _ptr(k8), _ptr(ksc), int(kstride), _ptr(cm), _stream(stream)), "lk_pf_qknr")
+
+
+class PrefillCtx:
+    """lk_pf_ctx: the prefill chunk driver's state (int8 K copies, k8_valid)."""
+
+    def __init__(self, n_layers, max_chunk, max_seq, attn8=True, ksmooth=False, near=1024, sink=1):
+        h = ctypes.c_void_p()
+        _check(load().lk_pf_ctx_create(int(n_layers), int(max_chunk), int(max_seq), int(bool(attn8)),
+                                       int(bool(ksmooth)), int(near), int(sink), ctypes.byref(h)),
+               "lk_pf_ctx_create")
+        self._h = h
+
+    def chunk_attn(self, layer, Y, qn, kn, m, pos0, kc, vc, o, stream=None) -> None:
+        _check(load().lk_pf_chunk_attn(self._h, int(layer), _ptr(Y), _ptr(qn), _ptr(kn), int(m), int(pos0),
+                                       _ptr(kc), _ptr(vc), _ptr(o), _stream(stream)), "lk_pf_chunk_attn")
+
+    def chunk_done(self, pos_end) -> None:
+        _check(load().lk_pf_chunk_done(self._h, int(pos_end)), "lk_pf_chunk_done")
+
+    def buffers(self, layer) -> dict:
+        qh, k8, ksc, cm = (ctypes.c_void_p() for _ in range(4))
+        ks, kv = ctypes.c_int(), ctypes.c_int()
+        _check(load().lk_pf_ctx_buffers(self._h, int(layer), ctypes.byref(qh), ctypes.byref(k8),
+                                        ctypes.byref(ksc), ctypes.byref(cm), ctypes.byref(ks),
+                                        ctypes.byref(kv)), "lk_pf_ctx_buffers")
+        return {"qh": qh.value, "k8": k8.value, "ksc": ksc.value, "cm": cm.value,
+                "kstride": ks.value, "k8_valid": kv.value}
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().lk_pf_ctx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -59,6 +59,12 @@ def test_host_argument_errors():
     assert lib.lk_pf_qknr(p, p, p, 4, 0, p, p, p, p, None, 8, None, None) == 1        # k8 without ksc
     assert lib.lk_pf_qknr(p, p, p, 4, 0, p, p, p, p, p, 6, None, None) == 1          # kstride % 4
     assert lib.lk_pf_qknr(None, None, None, 0, 0, None, None, None, None, None, 0, None, None) == 0
+    hc = ctypes.c_void_p()
+    assert lib.lk_pf_ctx_create(0, 16, 64, 1, 0, 0, 0, ctypes.byref(hc)) == 1
+    assert lib.lk_pf_ctx_create(1, 128, 64, 1, 0, 0, 0, ctypes.byref(hc)) == 1    # max_seq < max_chunk
+    assert lib.lk_pf_chunk_attn(None, 0, p, p, p, 4, 0, p, p, p, None) == 1
+    assert lib.lk_pf_chunk_done(None, 4) == 1
+    assert lib.lk_pf_ctx_destroy(None) == 0
     assert lib.lk_pf_split_override(-2) == 1
     assert lib.lk_pf_split_override(0) == 0
     # empty work is a successful no-op

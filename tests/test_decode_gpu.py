@@ -212,8 +212,8 @@ def test_config_c3_graph(lk, oracle):
 
 
 def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
-    """The decode step graph (per layer: stage, qk norm + RoPE + cache append,
-    split, combine; then d_pos += 1) replayed n times = n decode steps: cache
+    """The decode step graph (per layer: qk norm + RoPE + cache append, split,
+    combine; then d_pos += 1) replayed n times = n decode steps: cache
     rows, d_pos and every layer's output against the oracle, and the replay
     bit-identical to the same kernels called eagerly."""
     rng = np.random.default_rng(61)
@@ -239,7 +239,7 @@ def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
     d_pos = torch.tensor([P0], dtype=torch.int32, device="cuda")
     part = torch.empty(lk.part_bytes() // 4, device="cuda")
     g = lk.DecodeStepGraph(Ls, d_pos, part)
-    assert g.nodes() == 4 * layers + 1
+    assert g.nodes() == 3 * layers + 1
     g.run(steps)
     g.stream.synchronize()
     assert int(d_pos.item()) == P0 + steps
