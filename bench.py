@@ -182,6 +182,16 @@ def bench_prefill_c4(lk, lkc, iters):
     for _ in range(iters):
         f16()
     a16_ms = timed_events(f16, st, iters)
+    # the next GEMM's planar Q8_1: a separate pass over o, or fused (o not written)
+    aqs = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
+    asc = torch.empty(m, 64, 2, device="cuda")
+    fq = lambda: (f8(), lk.pf_quant_rows(o, m, 2048, 64, aqs, asc, stream=st))
+    ff = lambda: lk.pf_attn8_q81(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, None, aqs, asc, stream=st)
+    for f in (fq, ff):
+        for _ in range(iters):
+            f()
+    q_pass_ms = timed_events(fq, st, iters)
+    q_fused_ms = timed_events(ff, st, iters)
     oi, of, pairs = pf_ops(m, P)
     peak_ms = (oi / (PEAK_INT8_TOPS * 1e12) + of / (PEAK_FP16_TFLOPS * 1e12)) * 1e3
     return {
@@ -190,6 +200,7 @@ def bench_prefill_c4(lk, lkc, iters):
         "attn8_frac_of_mixed_peak": peak_ms / a8_ms,
         "attn_fp16_us": a16_ms * 1e3, "attn_fp16_TOPS": (oi + of) / (a16_ms * 1e-3) / 1e12,
         "q8_us": q_ms * 1e3, "k8_us": k_ms * 1e3,
+        "attn8_then_quant_rows_us": q_pass_ms * 1e3, "attn8_q81_fused_us": q_fused_ms * 1e3,
     }
 
 

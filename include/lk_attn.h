@@ -182,6 +182,27 @@ int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * qcs,
 int lk_pf_attn(const void * qh, int m, int P, const void * kc, const void * vc,
                float * o, void * stream);
 
+/* The same two attention kernels also emitting their output as planar Q8_1,
+ * the next GEMM's activation format (reference PfAct, prefill.cuh:27-36,
+ * produced there by a separate k_pf_quant_rows pass, engine.cu:1126): aqs int8
+ * [m][2048] and asc fp32 [m][64][2] = (float(fp16(d)), 8 * float(fp16(sum)))
+ * per 32-value block, byte-identical to lk_pf_quant_rows of o.  o may be NULL
+ * when aqs is given.  No counterpart in the reference: the quantisation pass
+ * fused into the attention epilogue. */
+int lk_pf_attn8_q81(const int8_t * q8, const float * qsc, const float * qcs,
+                    const void * qh, int m, int P, const int8_t * k8,
+                    const float * ksc, int kstride, const void * kc,
+                    const void * vc, int near, int sink, float * o,
+                    int8_t * aqs, float * asc, void * stream);
+int lk_pf_attn_q81(const void * qh, int m, int P, const void * kc, const void * vc,
+                   float * o, int8_t * aqs, float * asc, void * stream);
+
+/* Replaces k_pf_quant_rows (reference prefill.cuh:107, prefill.cu:1574-1580 with
+ * pf_quant_warp, prefill.cu:90-103): planar Q8_1 of fp32 rows X [rows][ld],
+ * kb 32-value blocks per row -> qs int8 [rows][kb*32], sc fp32 [rows][kb][2]. */
+int lk_pf_quant_rows(const float * X, int rows, int ld, int kb, int8_t * qs, float * sc,
+                     void * stream);
+
 /* Both attention entry points balance causal chunks by splitting the key range
  * of long query blocks across workgroups (merged by a second kernel, in a fixed
  * order: output stays run-to-run bit-identical).  The split uses a static
@@ -230,7 +251,9 @@ int lk_pf_qknr(const float * Y, const float * qn, const float * kn, int m, int P
  * copy caught up over [k8_valid, pos0) (keys decode steps appended since the
  * last prefill), the smoothing mean re-derived on a new context (pos0 == 0)
  * when ksmooth, the Q quantiser and the int8 (attn8 != 0) or fp16 attention
- * into o fp32 [m][2048].  lk_pf_chunk_done(pos0 + m) after the chunk's last
+ * into o fp32 [m][2048] and/or (aqs, asc) planar Q8_1 (see lk_pf_attn8_q81; the
+ * reference's k_pf_quant_rows that follows, engine.cu:1126, fused in; either
+ * output may be NULL, not both).  lk_pf_chunk_done(pos0 + m) after the chunk's last
  * layer sets k8_valid (engine.cu:1251).  create allocates the chunk buffers
  * and, per layer, the int8 K copy [max_seq][8][64], its scales and the mean
  * (engine.cu:974-985); nothing is allocated per call.  The chunking of a
@@ -242,7 +265,7 @@ int lk_pf_ctx_create(int n_layers, int max_chunk, int max_seq, int attn8, int ks
 int lk_pf_ctx_destroy(lk_pf_ctx * ctx);
 int lk_pf_chunk_attn(lk_pf_ctx * ctx, int layer, const float * Y, const float * qn,
                      const float * kn, int m, int pos0, void * kc, void * vc, float * o,
-                     void * stream);
+                     int8_t * aqs, float * asc, void * stream);
 int lk_pf_chunk_done(lk_pf_ctx * ctx, int pos_end);
 /* The context's device buffers for one layer (any output may be NULL). */
 int lk_pf_ctx_buffers(const lk_pf_ctx * ctx, int layer, void ** qh, int8_t ** k8,

@@ -7,7 +7,9 @@
 //   2. the int8 K copy caught up over [k8_valid, pos0) -- rows written by
 //      decode steps since the last prefill; a new context (pos0 == 0) with
 //      smoothing re-derives the mean vector from this chunk's keys first;
-//   3. lk_pf_q8, then lk_pf_attn8 (or lk_pf_attn with int8 scoring off).
+//   3. lk_pf_q8, then lk_pf_attn8 (or lk_pf_attn with int8 scoring off), the
+//      output as fp32 and/or planar Q8_1 (the reference's k_pf_quant_rows
+//      that follows, engine.cu:1126, fused into the attention epilogue).
 // lk_pf_chunk_done(pos0 + m) after the chunk's last layer moves k8_valid,
 // exactly where the reference does.  Buffers are allocated once, at create.
 #include "lk_common.h"
@@ -67,15 +69,16 @@ extern "C" int lk_pf_ctx_create(int n_layers, int max_chunk, int max_seq, int at
 extern "C" int lk_pf_ctx_destroy(lk_pf_ctx * ctx) { pf_ctx_free(ctx); return 0; }
 
 extern "C" int lk_pf_chunk_attn(lk_pf_ctx * c, int layer, const float * Y, const float * qn, const float * kn,
-                                int m, int pos0, void * kc, void * vc, float * o, void * stream) {
+                                int m, int pos0, void * kc, void * vc, float * o, int8_t * aqs, float * asc,
+                                void * stream) {
     if (!c || layer < 0 || layer >= c->n_layers || m <= 0 || m > c->max_chunk || pos0 < 0
-        || pos0 + m > c->max_seq || !Y || !qn || !kn || !kc || !vc || !o)
+        || pos0 + m > c->max_seq || !Y || !qn || !kn || !kc || !vc || (!o && !aqs) || (!aqs != !asc))
         return lk_fail(hipErrorInvalidValue, "lk_pf_chunk_attn: bad arguments (layer %d, m %d, pos0 %d)",
                        layer, m, pos0);
     int rc;
     if (!c->attn8) {
         rc = lk_pf_qknr(Y, qn, kn, m, pos0, c->qh, kc, vc, nullptr, nullptr, 0, nullptr, stream);
-        return rc ? rc : lk_pf_attn(c->qh, m, pos0, kc, vc, o, stream);
+        return rc ? rc : lk_pf_attn_q81(c->qh, m, pos0, kc, vc, o, aqs, asc, stream);
     }
     int8_t * k8 = c->k8[layer];
     float * ksc = c->ksc[layer];
@@ -96,8 +99,8 @@ extern "C" int lk_pf_chunk_attn(lk_pf_ctx * c, int layer, const float * Y, const
     if (rc) return rc;
     rc = lk_pf_q8(c->qh, m, cm, c->q8, c->qsc, c->qcs, stream);
     if (rc) return rc;
-    return lk_pf_attn8(c->q8, c->qsc, c->qcs, c->qh, m, pos0, k8, ksc, c->kstride, kc, vc,
-                       c->near, c->sink, o, stream);
+    return lk_pf_attn8_q81(c->q8, c->qsc, c->qcs, c->qh, m, pos0, k8, ksc, c->kstride, kc, vc,
+                           c->near, c->sink, o, aqs, asc, stream);
 }
 
 extern "C" int lk_pf_chunk_done(lk_pf_ctx * c, int pos_end) {

@@ -202,13 +202,65 @@ extern "C" int lk_pf_trace_read(void * dst, int n) {
 }
 #endif
 
+// ---- planar Q8_1 of the attention output (the next GEMM's input) -------------
+// Reference k_pf_quant_rows / pf_quant_warp (prefill.cu:1574-1580, 90-103): per
+// 32-value block am = max|x| (exact), sum = xor-butterfly over the block's
+// dims with strides 16, 8, 4, 2, 1, d = am/127 (IEEE), q = roundf(x/d) (0 when
+// am = 0), scale plane (float(fp16(d)), 8 * float(fp16(sum))).  Layout:
+// qs int8 [rows][2048] (block b of a row at 32b), sc float2 [rows][64].
+__device__ __forceinline__ float2 lk_q81_scales(float d, float sum) {
+    return make_float2((float) (_Float16) d, 8.0f * (float) (_Float16) sum);
+}
+__device__ __forceinline__ int8_t lk_q81_q(float x, float am, float d) {
+    return (am == 0.0f) ? (int8_t) 0 : (int8_t) roundf(x / d);
+}
+// From the attention epilogue's layout: lane (col, g) holds, for its query row,
+// dims 16db + 4g + r of the head (db, r = 0..3): block hb (dims 32hb ..
+// 32hb+31) is db = 2hb, 2hb+1 on the 4 lanes g of the row.  The sum follows
+// the reference's tree exactly: stride 16 = db pair (in lane), 8 and 4 = lanes
+// xor 32 and 16, 2 and 1 = r pairs (in lane).
+__device__ __forceinline__ void lk_pf_q81_epilogue(const lk_f4 (&a)[4], bool store, int8_t * __restrict__ qs,
+                                                   float2 * __restrict__ sc, int g) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+        const lk_f4 x0 = a[2 * hb], x1 = a[2 * hb + 1];
+        float am = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) am = fmaxf(am, fmaxf(fabsf(x0[r]), fabsf(x1[r])));
+        am = fmaxf(am, __shfl_xor(am, 32, 64));
+        am = fmaxf(am, __shfl_xor(am, 16, 64));
+        float t[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) t[r] = x0[r] + x1[r];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) t[r] += __shfl_xor(t[r], 32, 64);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) t[r] += __shfl_xor(t[r], 16, 64);
+        const float sum = (t[0] + t[2]) + (t[1] + t[3]);
+        const float d = am / 127.0f;
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            w0 |= (uint32_t) (uint8_t) lk_q81_q(x0[r], am, d) << (8 * r);
+            w1 |= (uint32_t) (uint8_t) lk_q81_q(x1[r], am, d) << (8 * r);
+        }
+        if (store) {
+            *(uint32_t *) (qs + 32 * hb + 4 * g)      = w0;
+            *(uint32_t *) (qs + 32 * hb + 16 + 4 * g) = w1;
+            if (g == 0) sc[hb] = lk_q81_scales(d, sum);
+        }
+    }
+}
+
 template <bool INT8>
 __global__ void __launch_bounds__(256, 2)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
              const float * __restrict__ qcs, const _Float16 * __restrict__ qh, int m, int P,
              const int8_t * __restrict__ k8, const float * __restrict__ ksc, int kstride,
              const _Float16 * __restrict__ kc, const _Float16 * __restrict__ vc,
-             int near, int sink, float * __restrict__ o, const PfWork work, float * __restrict__ pbuf) {
+             int near, int sink, float * __restrict__ o, int8_t * __restrict__ aqs,
+             float2 * __restrict__ asc, const PfWork work, float * __restrict__ pbuf) {
     __shared__ PfStage st[2];
     __shared__ __attribute__((aligned(16))) int8_t s_q[4][PF_BQ * PF_Q_LD];   // fp16 Q, per head
 #ifdef PF_WG_TRACE
@@ -577,26 +629,32 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     for (int qb = 0; qb < PF_QB; ++qb) {
         const float il = 1.0f / acc[4][qb][0];
         const int qr = qbase + 16 * qb + col;
-        if (qr < m) {
+        lk_f4 a[4];
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const lk_f4 a = acc[db][qb] * il;
+        for (int db = 0; db < 4; ++db) a[db] = acc[db][qb] * il;
+        if (o && qr < m) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
                 *(float4 *) (o + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 16 * db + 4 * g) =
-                    make_float4(a[0], a[1], a[2], a[3]);
-            }
+                    make_float4(a[db][0], a[db][1], a[db][2], a[db][3]);
         }
+        if (aqs) lk_pf_q81_epilogue(a, qr < m, aqs + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM,
+                                    asc + (size_t) qr * (LK_HIDDEN / 32) + 2 * head, g);
     }
     trace_end(kt_hi - kt_lo);
 }
 
 // Merge of the parts of split query blocks: workgroup (split block, kv head,
-// quarter of the dims), thread = (head, row) over 16 dims; the parts are
-// weighted 2^(m_p - M) with the exact max M and summed in part order.  All of
-// a thread's loads are independent, so it waits for memory about twice.
+// half of the dims), thread = (head, row) over 32 dims -- one Q8_1 block; the
+// parts are weighted 2^(m_p - M) with the exact max M and summed in part
+// order.  All of a thread's loads are independent, so it waits for memory
+// about twice.
 __global__ void __launch_bounds__(256)
-lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work, float * __restrict__ o) {
-    constexpr int MAXP = 8;                               // parts merged per pass
-    const int kvh = blockIdx.y, dq = blockIdx.z;          // dims 16dq .. 16dq+15
+lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work, float * __restrict__ o,
+                int8_t * __restrict__ aqs, float2 * __restrict__ asc) {
+#pragma clang fp contract(off)
+    constexpr int MAXP = 4;                               // parts merged per pass
+    const int kvh = blockIdx.y, hb = blockIdx.z;          // dims 32hb .. 32hb+31
     const int qt = work.split_qt[blockIdx.x];
     int np, per;
     pf_parts(qt, m, P, work.lsplit, np, per);
@@ -606,17 +664,17 @@ lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work
     if (qr >= m) return;
     auto base = [&](int p) { return pbuf + (size_t) ((slot + p) * LK_N_KV_HEADS + kvh) * PF_PART_SLOT; };
     float M = -INFINITY, L = 0.0f;
-    lk_f4 A[4] = {};
+    lk_f4 A[8] = {};
     for (int p0 = 0; p0 < np; p0 += MAXP) {
         float2 ml[MAXP];
-        lk_f4 a[MAXP][4];
+        lk_f4 a[MAXP][8];
 #pragma unroll
         for (int i = 0; i < MAXP; ++i) {
             const int p = (p0 + i < np) ? p0 + i : p0;    // clamped: loads stay in bounds
             ml[i] = ((const float2 *) (base(p) + PF_PART_ACC))[h * PF_BQ + row];
-            const lk_f4 * src = (const lk_f4 *) base(p) + (size_t) (h * 16 + 4 * dq) * PF_BQ + row;
+            const lk_f4 * src = (const lk_f4 *) base(p) + (size_t) (h * 16 + 8 * hb) * PF_BQ + row;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) a[i][c] = src[c * PF_BQ];
+            for (int c = 0; c < 8; ++c) a[i][c] = src[c * PF_BQ];
         }
         float Mn = M;
 #pragma unroll
@@ -624,24 +682,77 @@ lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work
         const float r = lk_exp2(M - Mn);                  // 0 on the first pass (M = -inf)
         L *= r;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) A[c] *= r;
+        for (int c = 0; c < 8; ++c) A[c] *= r;
 #pragma unroll
         for (int i = 0; i < MAXP; ++i) {
             if (p0 + i >= np) break;
             const float wgt = lk_exp2(ml[i].x - Mn);
             L += ml[i].y * wgt;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) A[c] += a[i][c] * wgt;
+            for (int c = 0; c < 8; ++c) A[c] += a[i][c] * wgt;
         }
         M = Mn;
     }
     const float il = 1.0f / L;
-    float * dst = o + (size_t) qr * LK_HIDDEN + (kvh * LK_G + h) * LK_HEAD_DIM + 16 * dq;
+    float x[32];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < 8; ++c) {
         const lk_f4 v = A[c] * il;
-        *(float4 *) (dst + 4 * c) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[4 * c + r] = v[r];
     }
+    const size_t col0 = (size_t) (kvh * LK_G + h) * LK_HEAD_DIM + 32 * hb;
+    if (o) {
+        float * dst = o + (size_t) qr * LK_HIDDEN + col0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) *(float4 *) (dst + 4 * c) = make_float4(x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]);
+    }
+    if (aqs) {                                            // the block's Q8_1, in-thread, same tree
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) am = fmaxf(am, fabsf(x[i]));
+        float t[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) t[i] = x[i];
+#pragma unroll
+        for (int st = 16; st > 0; st >>= 1)
+#pragma unroll
+            for (int i = 0; i < st; ++i) t[i] = t[i] + t[i + st];
+        const float d = am / 127.0f;
+        int8_t * q = aqs + (size_t) qr * LK_HIDDEN + col0;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) w |= (uint32_t) (uint8_t) lk_q81_q(x[4 * c + r], am, d) << (8 * r);
+            *(uint32_t *) (q + 4 * c) = w;
+        }
+        asc[(size_t) qr * (LK_HIDDEN / 32) + col0 / 32] = lk_q81_scales(d, t[0]);
+    }
+}
+
+// Standalone planar Q8_1 of fp32 rows (reference k_pf_quant_rows,
+// prefill.cu:1574-1580): grid (rows, ceil(kb/8)) x 256, one 32-lane half-wave
+// per (row, block), one value per lane; the sum tree is the lane butterfly
+// 16, 8, 4, 2, 1.
+__global__ void __launch_bounds__(256)
+lk_k_pf_quant_rows(const float * __restrict__ X, int ld, int kb, int8_t * __restrict__ qs,
+                   float2 * __restrict__ sc) {
+#pragma clang fp contract(off)
+    const int r = blockIdx.x;
+    const int b = blockIdx.y * 8 + (threadIdx.x >> 5), lane = threadIdx.x & 31;
+    const bool ok = b < kb;                               // half-wave uniform
+    const float x = ok ? X[(size_t) r * ld + b * 32 + lane] : 0.0f;
+    float am = fabsf(x), sum = x;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) {
+        am = fmaxf(am, __shfl_xor(am, o, 32));
+        sum += __shfl_xor(sum, o, 32);
+    }
+    const float d = am / 127.0f;
+    if (!ok) return;
+    qs[(size_t) r * kb * 32 + b * 32 + lane] = lk_q81_q(x, am, d);
+    if (lane == 0) sc[(size_t) r * kb + b] = lk_q81_scales(d, sum);
 }
 
 // Test hook: s[h][i][j] = int32 q8[i][h] . k8[j][h/4], one wave per 16x16 block.
@@ -785,49 +896,78 @@ template <bool INT8>
 static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qcs, const _Float16 * qh,
                           int m, int P, const int8_t * k8, const float * ksc, int kstride,
                           const _Float16 * kc, const _Float16 * vc, int near, int sink, float * o,
-                          hipStream_t st, const char * what) {
+                          int8_t * aqs, float2 * asc, hipStream_t st, const char * what) {
     PfWork wk;
     pf_plan(m, P, wk);
     if (wk.n_items == 0) {
         hipLaunchKernelGGL(lk_k_pf_attn<INT8>, dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0, st,
-                           q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, wk, (float *) nullptr);
+                           q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk,
+                           (float *) nullptr);
         return lk_launch_status(what);
     }
     int err = 0;
     float * pbuf = pf_part_ptr(err);
     if (!pbuf) return err;
     hipLaunchKernelGGL(lk_k_pf_attn<INT8>, dim3(wk.n_items * LK_N_KV_HEADS), dim3(256), 0, st,
-                       q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, wk, pbuf);
+                       q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk, pbuf);
     int rc = lk_launch_status(what);
     if (rc) return rc;
-    hipLaunchKernelGGL(lk_k_pf_combine, dim3(wk.n_split, LK_N_KV_HEADS, 4), dim3(256), 0, st,
-                       (const float *) pbuf, m, P, wk, o);
+    hipLaunchKernelGGL(lk_k_pf_combine, dim3(wk.n_split, LK_N_KV_HEADS, 2), dim3(256), 0, st,
+                       (const float *) pbuf, m, P, wk, o, aqs, asc);
     return lk_launch_status(what);
+}
+
+extern "C" int lk_pf_attn8_q81(const int8_t * q8, const float * qsc, const float * qcs,
+                               const void * qh, int m, int P, const int8_t * k8,
+                               const float * ksc, int kstride, const void * kc,
+                               const void * vc, int near, int sink, float * o,
+                               int8_t * aqs, float * asc, void * stream) {
+    if (m < 0 || P < 0) return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: m %d / P %d negative", m, P);
+    if (m == 0) return 0;
+    if (kstride % 4 != 0 || kstride < P + m)
+        return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: kstride %d must be a multiple of 4 and >= P+m %d", kstride, P + m);
+    if (!q8 || !qsc || !qh || !k8 || !ksc || !kc || !vc || (!o && !aqs) || (!aqs != !asc))
+        return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: null pointer argument");
+    return pf_attn_launch<true>(q8, qsc, qcs, (const _Float16 *) qh, m, P, k8, ksc, kstride,
+                                (const _Float16 *) kc, (const _Float16 *) vc, near, sink, o,
+                                aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn8");
 }
 
 extern "C" int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * qcs,
                            const void * qh, int m, int P, const int8_t * k8,
                            const float * ksc, int kstride, const void * kc,
                            const void * vc, int near, int sink, float * o, void * stream) {
-    if (m < 0 || P < 0) return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: m %d / P %d negative", m, P);
+    if (m > 0 && !o) return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: null pointer argument");
+    return lk_pf_attn8_q81(q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o,
+                           nullptr, nullptr, stream);
+}
+
+extern "C" int lk_pf_attn_q81(const void * qh, int m, int P, const void * kc, const void * vc,
+                              float * o, int8_t * aqs, float * asc, void * stream) {
+    if (m < 0 || P < 0) return lk_fail(hipErrorInvalidValue, "lk_pf_attn: m %d / P %d negative", m, P);
     if (m == 0) return 0;
-    if (kstride % 4 != 0 || kstride < P + m)
-        return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: kstride %d must be a multiple of 4 and >= P+m %d", kstride, P + m);
-    if (!q8 || !qsc || !qh || !k8 || !ksc || !kc || !vc || !o)
-        return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: null pointer argument");
-    return pf_attn_launch<true>(q8, qsc, qcs, (const _Float16 *) qh, m, P, k8, ksc, kstride,
-                                (const _Float16 *) kc, (const _Float16 *) vc, near, sink, o,
-                                lk_stream(stream), "lk_pf_attn8");
+    if (!qh || !kc || !vc || (!o && !aqs) || (!aqs != !asc))
+        return lk_fail(hipErrorInvalidValue, "lk_pf_attn: null pointer argument");
+    return pf_attn_launch<false>(nullptr, nullptr, nullptr, (const _Float16 *) qh, m, P, nullptr, nullptr, 0,
+                                 (const _Float16 *) kc, (const _Float16 *) vc, 0, 0, o,
+                                 aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn");
 }
 
 extern "C" int lk_pf_attn(const void * qh, int m, int P, const void * kc, const void * vc,
                           float * o, void * stream) {
-    if (m < 0 || P < 0) return lk_fail(hipErrorInvalidValue, "lk_pf_attn: m %d / P %d negative", m, P);
-    if (m == 0) return 0;
-    if (!qh || !kc || !vc || !o) return lk_fail(hipErrorInvalidValue, "lk_pf_attn: null pointer argument");
-    return pf_attn_launch<false>(nullptr, nullptr, nullptr, (const _Float16 *) qh, m, P, nullptr, nullptr, 0,
-                                 (const _Float16 *) kc, (const _Float16 *) vc, 0, 0, o,
-                                 lk_stream(stream), "lk_pf_attn");
+    if (m > 0 && !o) return lk_fail(hipErrorInvalidValue, "lk_pf_attn: null pointer argument");
+    return lk_pf_attn_q81(qh, m, P, kc, vc, o, nullptr, nullptr, stream);
+}
+
+extern "C" int lk_pf_quant_rows(const float * X, int rows, int ld, int kb, int8_t * qs, float * sc,
+                                void * stream) {
+    if (rows < 0 || kb < 0 || ld < kb * 32)
+        return lk_fail(hipErrorInvalidValue, "lk_pf_quant_rows: rows %d, kb %d, ld %d", rows, kb, ld);
+    if (rows == 0 || kb == 0) return 0;
+    if (!X || !qs || !sc) return lk_fail(hipErrorInvalidValue, "lk_pf_quant_rows: null pointer argument");
+    hipLaunchKernelGGL(lk_k_pf_quant_rows, dim3(rows, (kb + 7) / 8), dim3(256), 0, lk_stream(stream),
+                       X, ld, kb, qs, (float2 *) sc);
+    return lk_launch_status("lk_pf_quant_rows");
 }
 
 extern "C" int lk_pf_qk_i32(const int8_t * q8, int m, const int8_t * k8, int n,

@@ -32,6 +32,7 @@ EXPORTS = (
     "lk_pf_qk_i32", "lk_qk_norm_rope", "lk_pf_qknr",
     "lk_decode_step_graph_create", "lk_decode_graph_run",
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
+    "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows",
 )
 
 
@@ -82,7 +83,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_decode_graph_run": ([P, I, P], I),
         "lk_pf_ctx_create": ([I, I, I, I, I, I, I, P], I),
         "lk_pf_ctx_destroy": ([P], I),
-        "lk_pf_chunk_attn": ([P, I, P, P, P, I, I, P, P, P, P], I),
+        "lk_pf_chunk_attn": ([P, I, P, P, P, I, I, P, P, P, P, P, P], I),
+        "lk_pf_attn8_q81": ([P, P, P, P, I, I, P, P, I, P, P, I, I, P, P, P, P], I),
+        "lk_pf_attn_q81": ([P, I, I, P, P, P, P, P, P], I),
+        "lk_pf_quant_rows": ([P, I, I, I, P, P, P], I),
         "lk_pf_chunk_done": ([P, I], I),
         "lk_pf_ctx_buffers": ([P, I, P, P, P, P, P, P], I),
     }
@@ -277,6 +281,22 @@ def pf_attn(qh, m, P, kc, vc, o, stream=None) -> None:
     _check(load().lk_pf_attn(_ptr(qh), m, P, _ptr(kc), _ptr(vc), _ptr(o), _stream(stream)), "lk_pf_attn")
 
 
+def pf_attn8_q81(q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, stream=None) -> None:
+    _check(load().lk_pf_attn8_q81(_ptr(q8), _ptr(qsc), _ptr(qcs), _ptr(qh), int(m), int(P), _ptr(k8), _ptr(ksc),
+                                  int(kstride), _ptr(kc), _ptr(vc), int(near), int(sink), _ptr(o), _ptr(aqs),
+                                  _ptr(asc), _stream(stream)), "lk_pf_attn8_q81")
+
+
+def pf_attn_q81(qh, m, P, kc, vc, o, aqs, asc, stream=None) -> None:
+    _check(load().lk_pf_attn_q81(_ptr(qh), int(m), int(P), _ptr(kc), _ptr(vc), _ptr(o), _ptr(aqs), _ptr(asc),
+                                 _stream(stream)), "lk_pf_attn_q81")
+
+
+def pf_quant_rows(X, rows, ld, kb, qs, sc, stream=None) -> None:
+    _check(load().lk_pf_quant_rows(_ptr(X), int(rows), int(ld), int(kb), _ptr(qs), _ptr(sc), _stream(stream)),
+           "lk_pf_quant_rows")
+
+
 def pf_split_override(tiles: int) -> None:
     """-1 never split prefill blocks, 0 automatic, n > 0 parts of <= n key tiles."""
     _check(load().lk_pf_split_override(int(tiles)), "lk_pf_split_override")
@@ -312,9 +332,10 @@ class PrefillCtx:
                "lk_pf_ctx_create")
         self._h = h
 
-    def chunk_attn(self, layer, Y, qn, kn, m, pos0, kc, vc, o, stream=None) -> None:
+    def chunk_attn(self, layer, Y, qn, kn, m, pos0, kc, vc, o, aqs=None, asc=None, stream=None) -> None:
         _check(load().lk_pf_chunk_attn(self._h, int(layer), _ptr(Y), _ptr(qn), _ptr(kn), int(m), int(pos0),
-                                       _ptr(kc), _ptr(vc), _ptr(o), _stream(stream)), "lk_pf_chunk_attn")
+                                       _ptr(kc), _ptr(vc), _ptr(o), _ptr(aqs), _ptr(asc), _stream(stream)),
+               "lk_pf_chunk_attn")
 
     def chunk_done(self, pos_end) -> None:
         _check(load().lk_pf_chunk_done(self._h, int(pos_end)), "lk_pf_chunk_done")

@@ -427,6 +427,25 @@ void lko_mt_prefill_case(uint32_t seed, int m, int P, float koff, int with_off,
     }
 }
 
+// Planar Q8_1 of fp32 rows (reference k_pf_quant_rows, prefill.cu:1574-1580,
+// with pf_quant_warp, prefill.cu:90-103): per 32-value block the arithmetic of
+// lko_quantize_q8_1 (exact max, xor-butterfly sum 16..1, d = am/127, q =
+// roundf(x/d)); planes qs int8 [rows][kb*32], sc [rows][kb][2] =
+// (float(fp16(d)), 8 * float(fp16(sum))).
+void lko_pf_quant_rows(const float * X, int rows, int ld, int kb, int8_t * qs, float * sc) {
+    uint8_t blk[36];
+    for (int r = 0; r < rows; ++r)
+        for (int b = 0; b < kb; ++b) {
+            lko_quantize_q8_1(X + (size_t) r * ld + b * 32, blk);
+            std::memcpy(qs + ((size_t) r * kb + b) * 32, blk + 4, 32);
+            uint16_t dh, sh;
+            std::memcpy(&dh, blk, 2);
+            std::memcpy(&sh, blk + 2, 2);
+            sc[((size_t) r * kb + b) * 2]     = lko_h2f(dh);
+            sc[((size_t) r * kb + b) * 2 + 1] = 8.0f * lko_h2f(sh);
+        }
+}
+
 // ---------------------------------------------------------------------------
 // Attention-input producers: per-head RMS norm + NEOX rotary embedding of one
 // 64-wide row (reference kernels.cu:886-910 and prefill.cu:989-1009, identical

@@ -50,6 +50,7 @@ def load():
         "lko_pf_ref8": ([P, P, P, P, I, I, P, P, I, P, P, I, I, P, I, P], None),
         "lko_qk_i32": ([P, I, P, I, P], None),
         "lko_norm_rope_row": ([P, P, I, P], None),
+        "lko_pf_quant_rows": ([P, I, I, I, P, P], None),
         "lko_qk_norm_rope": ([P, P, P, P, P, I, P, P], None),
         "lko_pf_qknr": ([P, P, P, I, I, P, P, P], None),
         "lko_xs_fill_attn_case": ([P, S, P, P, P], None),
@@ -194,6 +195,15 @@ def qk_i32(q8, m, k8, n) -> np.ndarray:
     s = np.empty((32, m, n), np.int32)
     load().lko_qk_i32(_p(q8), m, _p(k8), n, _p(s))
     return s
+
+
+def pf_quant_rows(X, rows, ld, kb):
+    """Planar Q8_1 (qs int8 [rows][kb*32], sc fp32 [rows][kb][2])."""
+    X = np.ascontiguousarray(X, np.float32)
+    qs = np.empty((rows, kb * 32), np.int8)
+    sc = np.empty((rows, kb, 2), np.float32)
+    load().lko_pf_quant_rows(_p(X), int(rows), int(ld), int(kb), _p(qs), _p(sc))
+    return qs, sc
 
 
 # ---- attention-input producers (kernels.cu:871-915, prefill.cu:975-1016) ----------------

@@ -62,7 +62,10 @@ def test_host_argument_errors():
     hc = ctypes.c_void_p()
     assert lib.lk_pf_ctx_create(0, 16, 64, 1, 0, 0, 0, ctypes.byref(hc)) == 1
     assert lib.lk_pf_ctx_create(1, 128, 64, 1, 0, 0, 0, ctypes.byref(hc)) == 1    # max_seq < max_chunk
-    assert lib.lk_pf_chunk_attn(None, 0, p, p, p, 4, 0, p, p, p, None) == 1
+    assert lib.lk_pf_chunk_attn(None, 0, p, p, p, 4, 0, p, p, p, None, None, None) == 1
+    assert lib.lk_pf_attn8_q81(p, p, p, p, 4, 0, p, p, 8, p, p, 0, 0, None, p, None, None) == 1  # asc missing
+    assert lib.lk_pf_quant_rows(p, 2, 16, 1, p, p, None) == 1                                  # ld < 32 kb
+    assert lib.lk_pf_quant_rows(None, 0, 64, 2, None, None, None) == 0
     assert lib.lk_pf_chunk_done(None, 4) == 1
     assert lib.lk_pf_ctx_destroy(None) == 0
     assert lib.lk_pf_split_override(-2) == 1

@@ -451,3 +451,25 @@ def test_decode_and_prefill_producers_agree(oracle):
     # V is copied unnormalised and unrotated; rows outside [P, P+M) untouched
     assert np.array_equal(vc0.reshape(S, 8, 64)[P:], Y[:, 2560:].reshape(M, 8, 64).astype(np.float16).view(np.uint16))
     assert not kc0.reshape(S, 512)[:P].any()
+
+
+def test_pf_quant_rows_is_q8_1_widened(oracle):
+    # the planar format holds exactly block_q8_1's values (prefill.cuh:20-31)
+    rng = np.random.default_rng(11)
+    X = (rng.standard_normal((3, 96)) * 4).astype(np.float32)
+    X[1, 32:64] = 0.0                                 # an all-zero block
+    qs, sc = oracle.pf_quant_rows(X, 3, 96, 3)
+    for r in range(3):
+        for b in range(3):
+            blk = oracle.quantize_q8_1(X[r, 32 * b:32 * b + 32])
+            assert np.array_equal(qs[r, 32 * b:32 * b + 32], blk[4:].view(np.int8))
+            d, s = blk[:4].view(np.float16).astype(np.float32)
+            assert sc[r, b, 0] == d and sc[r, b, 1] == np.float32(8.0) * s
+    assert not qs[1, 32:64].any() and sc[1, 1, 0] == 0.0
+    # the q values reconstruct x to half a quantisation step
+    for r in range(3):
+        for b in range(3):
+            x = X[r, 32 * b:32 * b + 32]
+            d = np.abs(x).max() / np.float32(127.0)
+            if d > 0:
+                assert np.max(np.abs(qs[r, 32 * b:32 * b + 32] * d - x)) <= 0.5 * d * (1 + 1e-6)

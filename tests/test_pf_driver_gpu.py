@@ -57,8 +57,12 @@ def test_prefill_driver_two_chunks_with_decode_between(lk, oracle, smooth):
         for l in range(layers):
             Y = (rng.standard_normal((m, 3072)) * 3).astype(np.float32)
             o = torch.full((m, 2048), float("nan"), device="cuda")
-            ctx.chunk_attn(l, dev(Y), dev(W[l][0]), dev(W[l][1]), m, pos0, kc[l], vc[l], o)
+            aqs = torch.zeros(m, 2048, dtype=torch.int8, device="cuda")
+            asc = torch.zeros(m, 64, 2, device="cuda")
+            ctx.chunk_attn(l, dev(Y), dev(W[l][0]), dev(W[l][1]), m, pos0, kc[l], vc[l], o, aqs, asc)
             torch.cuda.synchronize()
+            qso, sco = oracle.pf_quant_rows(host(o), m, 2048, 64)   # the fused Q8_1 planes
+            assert np.array_equal(host(aqs), qso) and np.array_equal(host(asc).view(np.uint32), sco.view(np.uint32))
             # oracle, end to end
             qh = oracle.pf_qknr(Y, W[l][0], W[l][1], m, pos0, Kh[l].reshape(-1), Vh[l].reshape(-1))
             S = pos0 + m

@@ -270,3 +270,56 @@ def test_config_c5_last_chunk(lk, oracle):
     note("prefill config C5, last 4096 chunk at P=126976 (heavy-tailed Q/K)")
     qh, kc, vc, S = lk_configs.prefill_inputs("C5")
     _config_check(lk, oracle, qh, kc, vc, S - 4096, 4096, 1024, 1)
+
+
+# ---- planar Q8_1 of the attention output (reference k_pf_quant_rows) ----------------------------
+def test_quant_rows_bit_exact(lk, oracle):
+    rng = np.random.default_rng(81)
+    rows, ld, kb = 37, 2048, 64
+    X = (rng.standard_normal((rows, ld)) * rng.uniform(0.01, 5.0, (rows, 1))).astype(np.float32)
+    X[3, 64:96] = 0.0
+    note("pf quant_rows bit-exact")
+    qs = torch.zeros(rows, kb * 32, dtype=torch.int8, device="cuda")
+    sc = torch.zeros(rows, kb, 2, device="cuda")
+    lk.pf_quant_rows(dev(X), rows, ld, kb, qs, sc)
+    torch.cuda.synchronize()
+    qso, sco = oracle.pf_quant_rows(X, rows, ld, kb)
+    assert np.array_equal(host(qs), qso)
+    assert np.array_equal(host(sc).view(np.uint32), sco.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,P,near,L,int8", [(300, 700, 96, -1, True), (300, 0, 96, 2, True),
+                                             (129, 2000, 1024, 0, True), (300, 0, 0, 2, False)])
+def test_attn_fused_q81_equals_quant_rows(lk, oracle, m, P, near, L, int8):
+    K, V, Q = _inputs(oracle, m, P, 1.0, True)
+    sink = int(near > 0)
+    note(f"pf attn fused Q8_1 m={m} P={P} near={near} split={L} int8={int8}")
+    d = _Dev(lk, K, V, Q, m, P, False)
+    o = torch.full((m, 2048), float("nan"), device="cuda")
+    aqs = torch.zeros(m, 2048, dtype=torch.int8, device="cuda")
+    asc = torch.zeros(m, 64, 2, device="cuda")
+    try:
+        lk.pf_split_override(L)
+        if int8:
+            lk.pf_attn8_q81(d.q8, d.qsc, d.qcs, d.qh, m, P, d.k8, d.ksc, d.kstride, d.kc, d.vc, near, sink,
+                            o, aqs, asc)
+        else:
+            lk.pf_attn_q81(d.qh, m, P, d.kc, d.vc, o, aqs, asc)
+        # Q8_1 only (o = NULL) must give the same planes
+        aqs2 = torch.zeros_like(aqs)
+        asc2 = torch.zeros_like(asc)
+        if int8:
+            lk.pf_attn8_q81(d.q8, d.qsc, d.qcs, d.qh, m, P, d.k8, d.ksc, d.kstride, d.kc, d.vc, near, sink,
+                            None, aqs2, asc2)
+        else:
+            lk.pf_attn_q81(d.qh, m, P, d.kc, d.vc, None, aqs2, asc2)
+    finally:
+        lk.pf_split_override(0)
+    qs = torch.zeros_like(aqs)
+    sc = torch.zeros_like(asc)
+    lk.pf_quant_rows(o, m, 2048, 64, qs, sc)
+    torch.cuda.synchronize()
+    assert torch.equal(aqs, qs) and torch.equal(asc.view(torch.int32), sc.view(torch.int32))
+    assert torch.equal(aqs2, aqs) and torch.equal(asc2.view(torch.int32), asc.view(torch.int32))
+    qso, sco = oracle.pf_quant_rows(host(o), m, 2048, 64)
+    assert np.array_equal(host(aqs), qso) and np.array_equal(host(asc).view(np.uint32), sco.view(np.uint32))
