@@ -419,6 +419,10 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             qf8[qb] = zi; sq[qb] = 1.0f; isq[qb] = 1.0f; qc[qb] = 0.0f;
         }
     }
+    // exact tiles' score in units of 1/sq: (sum*log2e - qc) / sq as one fma
+    float exa[PF_QB], exb[PF_QB];
+#pragma unroll
+    for (int qb = 0; qb < PF_QB; ++qb) { exa[qb] = LK_LOG2E_F * isq[qb]; exb[qb] = -qc[qb] * isq[qb]; }
 
 
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
@@ -495,7 +499,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qa[j][1], c, 0, 0, 0);
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
-                            x[kb][j][i] = INT8 ? fmaf(c[i], LK_LOG2E_F, -qc[qb]) * isq[qb] : c[i] * LK_LOG2E_F;
+                            x[kb][j][i] = fmaf(c[i], exa[qb], exb[qb]);
                     }
                 }
             } else {
