@@ -153,6 +153,23 @@ __device__ __forceinline__ lk_i4 lk_mfma_qk8(lk_i4 kfrag, lk_i4 qfrag) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(kfrag, qfrag, z, 0, 0, 0);
 }
 
+// The same block with the accumulator seeded by the bit pattern of
+// PF_MAGIC = 1.5 * 2^23: |sum| <= 64 * 128 * 128 < 2^22, so the integer result
+// is the fp32 bit pattern of PF_MAGIC + sum, exactly (the float conversion done
+// by the integer add inside the MFMA).  sum * ks is then one fma,
+// fma(PF_MAGIC + sum, ks', -PF_MAGIC * ks'), exact in its product when ks' has
+// at most 22 significant bits: ks' = ks with the two low mantissa bits cleared
+// (a relative change below 2^-22, far inside the fp32 rounding of the score).
+constexpr float PF_MAGIC = 12582912.0f;                  // 0x4B400000
+__device__ __forceinline__ lk_f4 lk_mfma_qk8_magic(lk_i4 kfrag, lk_i4 qfrag) {
+    const int mb = 0x4B400000;
+    const lk_i4 z = { mb, mb, mb, mb };
+    return __builtin_bit_cast(lk_f4, __builtin_amdgcn_mfma_i32_16x16x64_i8(kfrag, qfrag, z, 0, 0, 0));
+}
+__device__ __forceinline__ float lk_pf_ks22(float ks) {
+    return __builtin_bit_cast(float, __builtin_bit_cast(unsigned, ks) & ~3u);
+}
+
 // ---- split-K work items (load balance of causal chunks) -----------------------
 // Query block qt of a chunk sees key tiles [0, nkt(qt)); with P = 0 that grows
 // from 1 to m/64 tiles, and a CU holding a long and a short block runs the
@@ -263,6 +280,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
              float2 * __restrict__ asc, const PfWork work, float * __restrict__ pbuf) {
     __shared__ PfStage st[2];
     __shared__ __attribute__((aligned(16))) int8_t s_q[4][PF_BQ * PF_Q_LD];   // fp16 Q, per head
+    __shared__ __attribute__((aligned(16))) float s_kp[4][2 * PF_BK];          // per wave: ks', -PF_MAGIC*ks'
 #ifdef PF_WG_TRACE
     const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
     auto trace_end = [&](int ntiles) {
@@ -356,30 +374,29 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             return;
         }
         // the block's last tile: keys past kend are clamped to kend-1 (valid
-        // memory, finite values); they are masked, so their p is exactly 0
-        const int last = kend - 1;
+        // memory, finite values); they are masked, so their p is exactly 0.
+        // Same tile bases as above, clamped rows in the per-lane offsets.
+        const int lim = kend - 1 - kb0;                   // >= 0: the tile holds a visible key
+        const int8_t * kb8 = k8 + (size_t) kb0 * LK_KV_ROW;
+        const _Float16 * kbh = kc + (size_t) kb0 * LK_KV_ROW;
+        const _Float16 * kbv = vc + (size_t) kb0 * LK_KV_ROW;
         if (md != PF_EXACT) {
-            const int r = 16 * w + (lane >> 2);
-            const int c = (lane & 3) ^ pf_sw_k8(r);
-            const int kp = (kb0 + r < last) ? kb0 + r : last;
-            lk_dma16c(k8 + ((size_t) kp * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 16 * c,
-                      sb + (uint32_t) (offsetof(PfStage, k8) + 1024 * w));
+            const int rr = (r_k8 < lim) ? r_k8 : lim;
+            lk_dma16c_so(kb8, so_k8 + (uint32_t) ((rr - r_k8) * LK_KV_ROW),
+                         sb + (uint32_t) (offsetof(PfStage, k8) + 1024 * w));
             if (lane < 4) {
-                const int s0 = kb0 + 16 * w + 4 * lane;
-                lk_dma16c(ks_h + (s0 < ks_clamp ? s0 : ks_clamp),
-                          sb + (uint32_t) (offsetof(PfStage, ks) + 64 * w));
+                const int s0 = 16 * w + 4 * lane, sl = ks_clamp - kb0;
+                lk_dma16c_so(ks_h + kb0, (uint32_t) (4 * (s0 < sl ? s0 : sl)),
+                             sb + (uint32_t) (offsetof(PfStage, ks) + 64 * w));
             }
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int r = 16 * w + 8 * j + (lane >> 3);
-            const int kp = (kb0 + r < last) ? kb0 + r : last;
-            const size_t row = ((size_t) kp * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM;
+            const uint32_t dr = (uint32_t) ((((r < lim) ? r : lim) - r) * LK_KV_ROW * 2);
             if (md != PF_INT8)
-                lk_dma16c(kc + row + 8 * ((lane & 7) ^ pf_sw_kh(r)),
-                          sb + (uint32_t) (offsetof(PfStage, kh) + 1024 * (2 * w + j)));
-            lk_dma16c(vc + row + 8 * ((lane & 7) ^ pf_sw_v(r)),
-                      sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * w + j)));
+                lk_dma16c_so(kbh, so_kh[j] + dr, sb + (uint32_t) (offsetof(PfStage, kh) + 1024 * (2 * w + j)));
+            lk_dma16c_so(kbv, so_v[j] + dr, sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * w + j)));
         }
     };
 
@@ -400,7 +417,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     }
     // ---- int8 Q operands and per-query scalars (lane column = query) ----------
     lk_i4 qf8[PF_QB];
-    float sq[PF_QB], isq[PF_QB], qc[PF_QB];
+    float sq[PF_QB], exa[PF_QB], exb[PF_QB];   // exa, exb: see below
 #pragma unroll
     for (int qb = 0; qb < PF_QB; ++qb) {
         const int qr = qbase + 16 * qb + col;
@@ -413,16 +430,15 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             // commute with the max); an all-zero query row has sq = 0 and zero
             // int8 scores, so unit scaling is exact for it
             sq[qb] = (d > 0.0f) ? d : 1.0f;
-            isq[qb] = 1.0f / sq[qb];
-            qc[qb] = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            // exact tiles' score in units of 1/sq: (sum*log2e - qc) / sq as one fma
+            const float isq = 1.0f / sq[qb];
+            const float qc = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            exa[qb] = LK_LOG2E_F * isq;
+            exb[qb] = -qc * isq;
         } else {
-            qf8[qb] = zi; sq[qb] = 1.0f; isq[qb] = 1.0f; qc[qb] = 0.0f;
+            qf8[qb] = zi; sq[qb] = 1.0f; exa[qb] = LK_LOG2E_F; exb[qb] = 0.0f;
         }
     }
-    // exact tiles' score in units of 1/sq: (sum*log2e - qc) / sq as one fma
-    float exa[PF_QB], exb[PF_QB];
-#pragma unroll
-    for (int qb = 0; qb < PF_QB; ++qb) { exa[qb] = LK_LOG2E_F * isq[qb]; exb[qb] = -qc[qb] * isq[qb]; }
 
 
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
@@ -464,12 +480,19 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         const bool msk = mask_of(kt);
         const int kb0 = kt * PF_BK;
         lk_i4 ka[4];                        // int8 K fragments (key row 16kb+col)
-        lk_f4 sk[4];                        // their scales (keys 16kb+4g+i)
+        lk_f4 sk[4], skb[4];                // scales (keys 16kb+4g+i), 22-bit, and -PF_MAGIC times them
         if (md != PF_EXACT) {
+            // the scale pair of the tile's 64 keys, one key per lane, through
+            // this wave's own LDS rows (LDS accesses of a wave complete in order)
+            const float s22 = lk_pf_ks22(S.ks[lane]);
+            s_kp[w][lane] = s22;
+            s_kp[w][PF_BK + lane] = s22 * -PF_MAGIC;
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
                 ka[kb] = *(const lk_i4 *) (S.k8 + o_k8 + 1024 * kb);
-                sk[kb] = *(const lk_f4 *) (S.ks + 16 * kb + 4 * g);
+                sk[kb] = *(const lk_f4 *) (&s_kp[w][16 * kb + 4 * g]);
+                skb[kb] = *(const lk_f4 *) (&s_kp[w][PF_BK + 16 * kb + 4 * g]);
             }
         }
         lk_h8 pb[PF_QB][2];
@@ -507,9 +530,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        const lk_i4 c = lk_mfma_qk8(ka[kb], qf8[2 * hq + j]);
+                        const lk_f4 c = lk_mfma_qk8_magic(ka[kb], qf8[2 * hq + j]);
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) x[kb][j][i] = (float) c[i] * sk[kb][i];
+                        for (int i = 0; i < 4; ++i) x[kb][j][i] = fmaf(c[i], sk[kb][i], skb[kb][i]);
                     }
             }
             if (msk) {
@@ -567,7 +590,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                         for (int i = 0; i < 4; ++i) v = fmaxf(v, x[kb][j][i]);
                     const float mx = lk_xrow_max(v);           // the 4 lane groups of this query
                     // key 0 is visible to every query, so mrun is finite after tile 0
-                    const bool need = mx > mrun[qb] + PF_HEADROOM * isq[qb];
+                    const bool need = (mx - mrun[qb]) * sq[qb] > PF_HEADROOM;
                     const float alpha = need ? lk_exp2((mrun[qb] - mx) * sq[qb]) : 1.0f;
                     mrun[qb] = need ? mx : mrun[qb];
 #pragma unroll
