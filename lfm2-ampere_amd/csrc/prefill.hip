@@ -455,10 +455,14 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     const _Float16 one = (_Float16) 1.0f;
     const lk_h8 ones = { one, one, one, one, one, one, one, one };
     // The running max is only raised when a score exceeds it by more than
-    // 2^PF_HEADROOM in p (so most tiles skip the rescale); p <= 2^8 stays far
-    // inside fp16 range and loses no relative precision.
+    // PF_HEADROOM (log2 units), so most tiles skip the rescale.  p is formed
+    // as 2^(sq*(x - m) - PF_P_BIAS): a score at the headroom limit gives
+    // p = 2^(8-7) = 2, the first fp16 value with bit 14 set, so "some p is past
+    // the limit (or inf/NaN)" is one bit of the OR of all p.  p <= 2 keeps fp16
+    // far from overflow; p stays normal down to 2^-21 of the running max.  The
+    // bias cancels in o = acc / l; partial records carry it in their max.
     constexpr float PF_HEADROOM = 8.0f;
-    constexpr unsigned PF_P_LIMIT_BITS = 0x5C00u;          // fp16 bits of 2^PF_HEADROOM = 256
+    constexpr float PF_P_BIAS = 7.0f;
 
     // ---- per-lane LDS read offsets: the swizzles above depend only on the lane
     // here, so every read below is one of these bases plus a constant.
@@ -547,17 +551,17 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                             if (16 * kb + i > dq) x[kb][j][i] = -INFINITY;
                 }
             }
-            // ---- online softmax, per query (lane column); exponent = sq*(x - m) --
+            // ---- online softmax, per query (lane column); exponent = sq*(x - m) - bias
             // p is formed against the running max first.  The exact tile max is
-            // only needed when some p would exceed 2^PF_HEADROOM (or the max is
-            // still -inf: first tile): that is detected on the fp16 bit patterns
-            // of p (p >= 0, so their u16 order is the f16 order, and inf/NaN
-            // sort above 2^8), two per lane op, with no cross-lane reduction.
+            // only needed when some score passes the headroom (or the max is
+            // still -inf: first tile): that is bit 14 of an fp16 p (p >= 2,
+            // inf or NaN), found in the OR of the p words, with no cross-lane
+            // reduction.
             auto make_p = [&]() {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int qb = 2 * hq + j;
-                    const float msq = mrun[qb] * sq[qb];
+                    const float msq = fmaf(mrun[qb], sq[qb], PF_P_BIAS);
 #pragma unroll
                     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -568,18 +572,21 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 }
             };
             make_p();
-            lk_u16x2 pm = { 0, 0 };
+            unsigned pw[16];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    const lk_u16x8 u = __builtin_bit_cast(lk_u16x8, pb[2 * hq + j][kk]);
+                    const lk_i4 u = __builtin_bit_cast(lk_i4, pb[2 * hq + j][kk]);
 #pragma unroll
-                    for (int e = 0; e < 8; e += 2)
-                        pm = __builtin_elementwise_max(pm, (lk_u16x2){ u[e], u[e + 1] });
+                    for (int e = 0; e < 4; ++e) pw[8 * j + 4 * kk + e] = (unsigned) u[e];
                 }
-            const unsigned pmax = (pm[0] > pm[1]) ? pm[0] : pm[1];
-            if (__ballot(pmax > PF_P_LIMIT_BITS)) {            // wave-uniform, rare
+#pragma unroll
+            for (int n = 16; n > 1; n = (n + 2) / 3)                // OR tree, three words per op
+#pragma unroll
+                for (int t = 0; t < (n + 2) / 3; ++t)
+                    pw[t] = pw[3 * t] | (3 * t + 1 < n ? pw[3 * t + 1] : 0u) | (3 * t + 2 < n ? pw[3 * t + 2] : 0u);
+            if (__ballot(pw[0] & 0x40004000u)) {               // wave-uniform, rare
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int qb = 2 * hq + j;
@@ -645,7 +652,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             const int row = 16 * qb + col;
 #pragma unroll
             for (int db = 0; db < 4; ++db) A[(4 * db + g) * PF_BQ + row] = acc[db][qb];
-            if (g == 0) ML[row] = make_float2(mrun[qb] * sq[qb], acc[4][qb][0]);
+            if (g == 0) ML[row] = make_float2(fmaf(mrun[qb], sq[qb], PF_P_BIAS), acc[4][qb][0]);
         }
         trace_end(kt_hi - kt_lo);
         return;
