@@ -70,13 +70,17 @@ const char * lk_last_error(void);
 
 /* Replaces k_attn_split (reference kernels.cuh:647-649, kernels.cu:1303-1556).
  * Grid (split_cap) of 8-wave workgroups, each over all 8 kv heads of one
- * contiguous slice of positions; workgroups past the live slice count exit. */
+ * contiguous slice of positions; workgroups past the live slice count write
+ * the neutral record (m = -inf, l = 0, acc = 0) of their slot and exit, so
+ * every one of the split_cap slots of part is valid afterwards. */
 int lk_attn_split(const float * q, const void * kc, const void * vc,
                   const int * d_pos, float * part, void * stream);
 
 /* Replaces k_attn_combine (reference kernels.cuh:650-652, kernels.cu:1558-1599).
- * Slice partials are merged in a fixed order, so output is run-to-run
- * bit-identical. */
+ * All split_cap slots of part (as lk_attn_split leaves them) are merged in a
+ * fixed order, so output is run-to-run bit-identical.  d_pos is not read (the
+ * neutral records carry weight exactly 0); the argument keeps the reference's
+ * signature. */
 int lk_attn_combine(const float * part, const int * d_pos, float * out,
                     lk_block_q8_1 * yq8, void * stream);
 

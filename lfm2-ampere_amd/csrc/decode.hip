@@ -69,9 +69,17 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
     const int sp = blockIdx.x;
     const int t0 = sp * chunk;
     const int t1 = (t0 + chunk < seq) ? (t0 + chunk) : seq;
-    // Block-uniform early out before any barrier: dead slices write nothing
-    // (the combine derives the same boundary and never reads them).
-    if (t0 >= t1) return;
+    // Block-uniform early out before any barrier: a dead slice writes the
+    // neutral record (m = -inf, l = 0, acc = 0) of each query head, so every
+    // slot the combine reads is valid without it knowing seq.
+    if (t0 >= t1) {
+        for (int i = threadIdx.x; i < LK_N_HEADS * (LK_ATTN_PARTW / 4); i += LK_DEC_THREADS) {
+            const int h = i / (LK_ATTN_PARTW / 4), k = i % (LK_ATTN_PARTW / 4);
+            *(lk_f4 *) (part + ((size_t) h * LK_ATTN_SPLIT + sp) * LK_ATTN_PARTW + 4 * k) =
+                (lk_f4){ k == 0 ? -INFINITY : 0.0f, 0.0f, 0.0f, 0.0f };
+        }
+        return;
+    }
     const int n = t1 - t0;
     const int ntile = (n + LK_DEC_TILE - 1) / LK_DEC_TILE;
 
@@ -274,11 +282,6 @@ __device__ __forceinline__ void lk_quant_q8_1_half(float x, lk_block_q8_1 * __re
     }
 }
 
-// Combine: grid (32 query heads, 2 halves of the 64 dims), 256 threads.
-// Slices s with s*chunk >= seq hold no tokens and are skipped (reference
-// kernels.cu:1573-1584).  Every lane requests its slices' (m, l) and values at
-// once (one memory round trip), the max M is exact, the slice weights are
-// 2^(m_s - M).  Each half is exactly one Q8_1 block of the next GEMV's input.
 // Sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the gfx950
 // lane swaps; like lk_xrow_max, every lane ends with identical bits.
 #ifdef __HIP_DEVICE_COMPILE__
@@ -293,46 +296,49 @@ __device__ __forceinline__ float lk_xrow_sum(float x) {
 __device__ __forceinline__ float lk_xrow_sum(float x) { return x; }
 #endif
 
-// Combine: workgroup (head, half) produces 32 output dims; wave w owns dims
-// 32*half + 8w .. +7 over all slices, lane l the slices l, l+64, l+128, l+192.
-// Every sum runs in a fixed order (per lane in slice order, then a fixed
-// lane tree), so the output is run-to-run bit-identical.
-static_assert(LK_ATTN_SPLIT <= 256, "combine: at most 4 slices per lane");
+// Combine: grid (32 query heads, 2 halves of the 64 dims), 256 threads;
+// workgroup (head, half) produces 32 output dims, wave w owns dims
+// 32*half + 8w .. +7 over all slots, lane l the slots l, l+64, l+128, l+192.
+// Slices s with s*chunk >= seq hold no tokens (reference kernels.cu:1573-1584);
+// their workgroups wrote the neutral record (m = -inf, l = 0, acc = 0), whose
+// weight 2^(-inf - M) is exactly 0, so every slot is merged and d_pos is not
+// read: all of a lane's loads go out at once, one memory round trip.  The max
+// M is exact, the slot weights are 2^(m_s - M).  Every sum runs in a fixed
+// order (per lane in slot order, then a fixed lane tree), so the output is
+// run-to-run bit-identical.  Each half is exactly one Q8_1 block of the next
+// GEMV's input.
+static_assert(LK_ATTN_SPLIT <= 256 && LK_ATTN_SPLIT % 64 == 0, "combine: 1-4 whole slots per lane");
 __global__ void __launch_bounds__(256)
 lk_k_attn_combine(const float * __restrict__ part, const int * __restrict__ d_pos,
                   float * __restrict__ out, lk_block_q8_1 * __restrict__ yq8) {
-    constexpr int J = (LK_ATTN_SPLIT + 63) / 64;
+    (void) d_pos;
+    constexpr int J = LK_ATTN_SPLIT / 64;
     const int head = blockIdx.x, half = blockIdx.y;
-    const int seq = *d_pos + 1;
-    int ns, chunk;
-    lk_attn_slices(seq, ns, chunk);
-    const int nv = (seq + chunk - 1) / chunk;        // non-empty slices, <= ns
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int d0 = 32 * half + 8 * wv;
 
-    float m[J], l[J];
+    // (m, l) as a float2: a 16-byte load whose pad lanes are dead lets the
+    // register allocator reuse them while the load is in flight, which costs a
+    // full vmcnt wait per record
+    float2 ml[J];
     lk_f4 a0[J], a1[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const int s = lane + 64 * j;
-        const bool live = s < nv;
-        const float * R = part + ((size_t) head * LK_ATTN_SPLIT + (live ? s : 0)) * LK_ATTN_PARTW;
-        const lk_f4 ml = *(const lk_f4 *) R;         // m, l, pad, pad
+        const float * R = part + ((size_t) head * LK_ATTN_SPLIT + lane + 64 * j) * LK_ATTN_PARTW;
+        ml[j] = *(const float2 *) R;                 // m, l (then two pad floats)
         a0[j] = *(const lk_f4 *) (R + 4 + d0);
         a1[j] = *(const lk_f4 *) (R + 8 + d0);
-        m[j] = live ? ml[0] : -1e30f;
-        l[j] = live ? ml[1] : 0.0f;
     }
-    float M = m[0];
+    float M = ml[0].x;
 #pragma unroll
-    for (int j = 1; j < J; ++j) M = fmaxf(M, m[j]);
-    M = lk_xrow_max(lk_row_max16(M));
+    for (int j = 1; j < J; ++j) M = fmaxf(M, ml[j].x);
+    M = lk_xrow_max(lk_row_max16(M));                // finite: slice 0 always holds tokens
     float L = 0.0f;
     lk_f4 A0 = { 0.f, 0.f, 0.f, 0.f }, A1 = A0;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const float e = lk_exp2(m[j] - M);           // dead slices: exp2(-1e30 - M) = 0
-        L += l[j] * e;
+        const float e = lk_exp2(ml[j].x - M);        // neutral records: exactly 0
+        L += ml[j].y * e;
         A0 += a0[j] * e;
         A1 += a1[j] * e;
     }

@@ -133,6 +133,26 @@ def test_null_outputs_and_q8_only(lk, oracle):
     assert torch.equal(y1, y2)
 
 
+@pytest.mark.parametrize("seq", [1, 9, 17, 1025, 1031])
+def test_dead_slices_write_neutral_records(lk, oracle, seq):
+    """Lengths whose slice plan leaves empty slices (seq / ceil(seq / ns) < ns,
+    and every slot past ns): the partial buffer starts as NaN everywhere, the
+    combine merges all slots, and the result is the float64 reference's."""
+    rng = np.random.default_rng(seq)
+    q = rng.standard_normal((32, 64)).astype(np.float32)
+    kc = rng.standard_normal((seq, 8, 64)).astype(np.float16)
+    vc = rng.standard_normal((seq, 8, 64)).astype(np.float16)
+    part = torch.full((lk.part_bytes() // 4,), float("nan"), device="cuda")
+    out = torch.full((32, 64), float("nan"), device="cuda")
+    note(f"decode dead slices seq={seq}")
+    lk.attn_decode(dev(q), dev_h(kc.view(np.uint16)), dev_h(vc.view(np.uint16)), d_pos_for(seq), part, out, None)
+    torch.cuda.synchronize()
+    ref = oracle.decode_ref(q, kc.view(np.uint16), vc.view(np.uint16), seq)
+    o = host(out)
+    assert np.isfinite(o).all()
+    assert abs_err(o, ref) <= 1e-3
+
+
 def test_serial_beyond_limit_writes_nothing(lk):
     seq = lk.DECODE_MAX_SEQ + 1
     q = torch.randn(32, 64, device="cuda")
