@@ -141,7 +141,7 @@ __device__ __forceinline__ int pf_sw_v(int r)  { return ((r >> 1) & 3) << 1; }
 // Exact-tile predicate of the reference (prefill.cu:1380-1382), stated on its
 // 64-key tiles: tile kt64 is exact for the 32-query tile qt32 iff
 // kt64*64 + 64 > P + qt32*32 - near, or sink and kt64 == 0.
-__device__ __forceinline__ bool lk_pf_exact(int P, int qt32, int kt64, int near, int sink) {
+__host__ __device__ __forceinline__ bool lk_pf_exact(int P, int qt32, int kt64, int near, int sink) {
     return (kt64 * 64 + 64 > P + qt32 * 32 - near) || (sink && kt64 == 0);
 }
 
@@ -172,18 +172,18 @@ __device__ __forceinline__ float lk_pf_ks22(float ks) {
 
 // ---- split-K work items (load balance of causal chunks) -----------------------
 // Query block qt of a chunk sees key tiles [0, nkt(qt)); with P = 0 that grows
-// from 1 to m/64 tiles, and a CU holding a long and a short block runs the
-// long one's tail at one wave per SIMD (about half speed).  With lsplit > 0,
-// blocks longer than lsplit tiles are cut into np near-equal key ranges
-// ("parts"), every part writes an unnormalised partial (m, l, acc) and
-// lk_k_pf_combine merges them in part order.  Items are enumerated longest
-// block first (kv head fastest), so the hardware dispatcher hands out the big
-// items first.  A part never starts after the block's first diagonal tile,
-// so every query sees at least one key in every part.
+// from 1 to m/64 tiles.  Work items are key ranges [kt_lo, kt_hi) of a block;
+// a block cut into several ("parts") has every part write an unnormalised
+// partial (m, l, acc), which lk_k_pf_combine merges in part order.  A part
+// never starts after the block's first diagonal tile, so every query sees at
+// least one key in every part.  The grid enumerates items with the kv head
+// fastest, and the dispatcher sends kv head x of every item to XCD x: each
+// XCD runs the same item sequence, greedily, on its slots.
 __host__ __device__ inline int pf_nkt(int qt, int m, int P) {
     const int qlast = (qt * PF_BQ + PF_BQ < m) ? qt * PF_BQ + PF_BQ : m;
     return (P + qlast + PF_BK - 1) / PF_BK;
 }
+// Equal-size parts of at most lsplit tiles (the test hook's plan).
 __host__ __device__ inline void pf_parts(int qt, int m, int P, int lsplit, int & np, int & per) {
     const int nkt = pf_nkt(qt, m, P);
     np = (lsplit > 0) ? (nkt + lsplit - 1) / lsplit : 1;
@@ -192,16 +192,19 @@ __host__ __device__ inline void pf_parts(int qt, int m, int P, int lsplit, int &
     const int kdiag = (P + qt * PF_BQ) / PF_BK;        // tile holding the block's first query
     while (np > 1 && (np - 1) * per > kdiag) { --np; per = (nkt + np - 1) / np; }
 }
-// The launch's work list, built on the host and passed by value: items sorted
-// longest first (kv head fastest in the grid), each = (block, part); slot0[q]
-// is the first partial slot of split block q; split_qt lists the split blocks.
-#define PF_MAX_ITEMS 640
+// The launch's work list, built on the host and passed by value (two 32-bit
+// words per item, read with uniform scalar loads): items in dispatch order;
+// slot0[q] is the first partial slot of split block q, nparts[q] its part
+// count; split_qt lists the split blocks.
+#define PF_MAX_ITEMS 384
 #define PF_MAX_QB    128
 struct PfWork {
-    int n_items, n_split, lsplit;                      // n_items 0: unsplit launch
-    uint16_t item[PF_MAX_ITEMS];                        // qt | part << 8
+    int n_items, n_split;                              // n_items 0: unsplit launch
+    uint32_t item[PF_MAX_ITEMS];                       // qt | (partial slot + 1) << 16 (0: not split)
+    uint32_t krange[PF_MAX_ITEMS];                     // kt_lo | kt_hi << 16
     int16_t slot0[PF_MAX_QB];
     uint8_t split_qt[PF_MAX_QB];
+    uint8_t nparts[PF_MAX_QB];
 };
 // Partials of a part, per (slot, kv head): acc as [head][16 dim chunks][64
 // rows] of float4 (coalesced for the writing lanes and the merging lanes),
@@ -308,16 +311,16 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         kt_lo = 0; kt_hi = pf_nkt(qt, m, P);
     } else {
         kvh = blockIdx.x % LK_N_KV_HEADS;
-        const int it = work.item[blockIdx.x / LK_N_KV_HEADS];
-        qt = it & 255;
-        const int part = it >> 8;
-        int np, per;
-        pf_parts(qt, m, P, work.lsplit, np, per);
-        kt_lo = part * per;
-        kt_hi = pf_nkt(qt, m, P);
-        if (kt_lo + per < kt_hi) kt_hi = kt_lo + per;
-        if (np > 1) pslot = work.slot0[qt] + part;
+        const int i = blockIdx.x / LK_N_KV_HEADS;
+        const uint32_t it = work.item[i], kr = work.krange[i];
+        qt = (int) (it & 255);
+        pslot = (int) (it >> 16) - 1;
+        kt_lo = (int) (kr & 0xffff);
+        kt_hi = (int) (kr >> 16);
     }
+#ifdef PF_WG_TRACE
+    const uint64_t t_w = __builtin_amdgcn_s_memrealtime();
+#endif
     const int tid  = threadIdx.x;
     const int lane = tid & 63;
     const int w    = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -404,16 +407,16 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // memory latencies overlap.
     issue(kt_lo);
 
-    // ---- this wave's fp16 Q block (64 rows x 128 B) into LDS, for exact tiles --
-    {
-        const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
+    // ---- this wave's fp16 Q block (64 rows x 128 B), for exact tiles, and the
+    // int8 Q operands and scales below.  Every load reads a row clamped to m-1
+    // and rows past m are zeroed by a select afterwards (a guarded load costs a
+    // branch and a full memory wait each), and all of them are issued before
+    // the first use: one memory round trip for the whole prologue.
+    lk_h8 qv16[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = (lane >> 3) + 8 * i, c = lane & 7;
-            const int qr = qbase + r;
-            const lk_h8 v = (qr < m) ? *(const lk_h8 *) (qh + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 8 * c) : z8;
-            *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * c) = v;
-        }
+    for (int i = 0; i < 8; ++i) {
+        const int qr = qbase + (lane >> 3) + 8 * i;
+        qv16[i] = *(const lk_h8 *) (qh + (size_t) (qr < m ? qr : m - 1) * LK_HIDDEN + head * LK_HEAD_DIM + 8 * (lane & 7));
     }
     // ---- int8 Q operands and per-query scalars (lane column = query) ----------
     lk_i4 qf8[PF_QB];
@@ -422,25 +425,40 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     for (int qb = 0; qb < PF_QB; ++qb) {
         const int qr = qbase + 16 * qb + col;
         const bool ok = qr < m;
+        const int qrc = ok ? qr : m - 1;                  // clamped: unconditional loads
         const lk_i4 zi = { 0, 0, 0, 0 };
         if (INT8) {
-            qf8[qb] = ok ? *(const lk_i4 *) (q8 + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 16 * g) : zi;
-            const float d = ok ? qsc[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            const lk_i4 qv = *(const lk_i4 *) (q8 + (size_t) qrc * LK_HIDDEN + head * LK_HEAD_DIM + 16 * g);
+            const float dv = qsc[(size_t) qrc * LK_N_HEADS + head];
+            const float cv = qcs ? qcs[(size_t) qrc * LK_N_HEADS + head] : 0.0f;
+            qf8[qb] = ok ? qv : zi;
+            const float d = ok ? dv : 0.0f;
             // scores are kept in units of 1/sq until the exponent (sq > 0 scales
             // commute with the max); an all-zero query row has sq = 0 and zero
             // int8 scores, so unit scaling is exact for it
             sq[qb] = (d > 0.0f) ? d : 1.0f;
             // exact tiles' score in units of 1/sq: (sum*log2e - qc) / sq as one fma
             const float isq = 1.0f / sq[qb];
-            const float qc = (ok && qcs) ? qcs[(size_t) qr * LK_N_HEADS + head] : 0.0f;
+            const float qc = ok ? cv : 0.0f;
             exa[qb] = LK_LOG2E_F * isq;
             exb[qb] = -qc * isq;
         } else {
             qf8[qb] = zi; sq[qb] = 1.0f; exa[qb] = LK_LOG2E_F; exb[qb] = 0.0f;
         }
     }
+    {
+        const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = (lane >> 3) + 8 * i;
+            *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * (lane & 7)) = (qbase + r < m) ? qv16[i] : z8;
+        }
+    }
 
 
+#ifdef PF_WG_TRACE
+    const uint64_t t_q = __builtin_amdgcn_s_memrealtime();
+#endif
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
     // all-ones A operand, so every lane of query column q accumulates
     // l_q = sum of the same fp16 P the numerator uses.
@@ -640,7 +658,8 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     }
 #ifdef PF_WG_TRACE
     if (threadIdx.x == 0 && blockIdx.x + blockIdx.y * gridDim.x < 8192)
-        g_pf_trace[8192 + blockIdx.x + blockIdx.y * gridDim.x] = make_uint4((unsigned) t_a, (unsigned) t_b, (unsigned) t_c, 0u);
+        g_pf_trace[8192 + blockIdx.x + blockIdx.y * gridDim.x] = make_uint4((unsigned) t_a, (unsigned) t_b, (unsigned) t_c,
+                                                                        (unsigned) ((t_w - t_start) & 0xffff) | ((unsigned) ((t_q - t_start) & 0xffff) << 16));
 #endif
 
     if (pslot >= 0) {                                     // a part: unnormalised partial
@@ -690,8 +709,7 @@ lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work
     constexpr int MAXP = 4;                               // parts merged per pass
     const int kvh = blockIdx.y, hb = blockIdx.z;          // dims 32hb .. 32hb+31
     const int qt = work.split_qt[blockIdx.x];
-    int np, per;
-    pf_parts(qt, m, P, work.lsplit, np, per);
+    const int np = work.nparts[qt];
     const int slot = work.slot0[qt];
     const int row = threadIdx.x & 63, h = threadIdx.x >> 6;
     const int qr = qt * PF_BQ + row;
@@ -876,54 +894,106 @@ static int pf_slots_per_device() {
 }
 
 // The work list of this chunk: n_items = 0 for an unsplit launch.
-static void pf_plan(int m, int P, PfWork & wk) {
-    wk.n_items = 0; wk.n_split = 0; wk.lsplit = 0;
+//
+// Automatic plan.  Cost model, in units of one int8 tile on a CU shared by
+// two workgroups (from per-workgroup timestamps on MI355X): int8 tile 1,
+// exact or mixed tile 1.4, start-up of a workgroup 2.1.  T = total cost / the
+// slots one kv head gets (a slot: one of the two workgroups of a CU).  When
+// the costliest block exceeds 1.25 T (a causal chunk with P small against
+// m), every block costlier than T is cut into pieces of cost T, from its
+// first tile on, and the rest; items are dispatched costliest first, so the
+// remainders and the short blocks fill the slots that free up early.  (A
+// dispatch simulation calibrated on the measured spans of the C4 chunk: 113 ->
+// 100 us, the floor being ~89.)  T grows when the parts would not fit the
+// partial buffer or the item list.
+#ifndef PF_PLAN_T
+#define PF_PLAN_T 1.0f      // piece cost, in units of the mean cost per slot
+#endif
+static void pf_plan(int m, int P, int near, int sink, bool int8, PfWork & wk) {
+    wk.n_items = 0; wk.n_split = 0;
     const int nq = (m + PF_BQ - 1) / PF_BQ;
     if (g_pf_split_override < 0 || nq > PF_MAX_QB) return;
-    long total = 0;
-    for (int qt = 0; qt < nq; ++qt) total += pf_nkt(qt, m, P);
-    const int nkt_max = pf_nkt(nq - 1, m, P);
-    int L;
-    if (g_pf_split_override > 0) L = g_pf_split_override;
-    else {
-        const long slots = pf_slots_per_device();
-        // target 1.5x the mean work per workgroup slot: finer parts measured
-        // slower (each workgroup pays a few microseconds of start-up)
-        L = (int) ((3 * total * LK_N_KV_HEADS + 2 * slots - 1) / (2 * slots));
-        if (L < 8) L = 8;
-        if (4 * nkt_max <= 5 * L) return;                 // longest block within 1.25x of the target
-    }
-    for (;; L *= 2) {
-        if (L >= nkt_max) return;
-        int items = 0, parts = 0, nsplit = 0;
-        for (int qt = 0; qt < nq; ++qt) {
-            int np, per;
-            pf_parts(qt, m, P, L, np, per);
-            items += np;
-            if (np > 1) { parts += np; ++nsplit; }
+    auto tcost = [&](int qt, int kt) -> float {
+        return (!int8 || lk_pf_exact(P, 2 * qt, kt, near, sink)) ? 1.4f : 1.0f;
+    };
+    constexpr float START = 2.1f;
+    constexpr int MAXP = 64;                           // pieces per block
+    int cut[PF_MAX_QB][MAXP + 1];                      // piece boundaries per block
+    int npc[PF_MAX_QB];
+    auto fits = [&]() {
+        int items = 0, parts = 0;
+        for (int qt = 0; qt < nq; ++qt) { items += npc[qt]; if (npc[qt] > 1) parts += npc[qt]; }
+        return items <= PF_MAX_ITEMS && (size_t) parts * LK_N_KV_HEADS * PF_PART_SLOT <= PF_PART_CAP;
+    };
+    if (g_pf_split_override > 0) {                     // equal parts of at most L tiles
+        for (int L = g_pf_split_override;; L *= 2) {
+            bool ok = true;
+            for (int qt = 0; qt < nq; ++qt) {
+                int np, per;
+                pf_parts(qt, m, P, L, np, per);
+                const int nkt = pf_nkt(qt, m, P);
+                if (np > MAXP) { np = 1; per = nkt; ok = false; }
+                npc[qt] = np;
+                for (int p = 0; p <= np; ++p) cut[qt][p] = (p * per < nkt) ? p * per : nkt;
+            }
+            if (ok && fits()) break;
         }
-        if (nsplit == 0) return;
-        if (items <= PF_MAX_ITEMS && (size_t) parts * LK_N_KV_HEADS * PF_PART_SLOT <= PF_PART_CAP) break;
+    } else {
+        float total = 0.0f, cmax = 0.0f;
+        float bc[PF_MAX_QB];
+        for (int qt = 0; qt < nq; ++qt) {
+            bc[qt] = START;
+            for (int kt = 0; kt < pf_nkt(qt, m, P); ++kt) bc[qt] += tcost(qt, kt);
+            total += bc[qt];
+            cmax = (bc[qt] > cmax) ? bc[qt] : cmax;
+        }
+        float T = PF_PLAN_T * total * LK_N_KV_HEADS / (float) pf_slots_per_device();
+        if (T < 8.0f) T = 8.0f;
+        if (cmax <= 1.25f * T) return;
+        for (;; T *= 1.25f) {
+            for (int qt = 0; qt < nq; ++qt) {
+                const int nkt = pf_nkt(qt, m, P);
+                const int kdiag = (P + qt * PF_BQ) / PF_BK;
+                int np = 0;
+                cut[qt][np] = 0;
+                float c = START;
+                for (int kt = 0; kt < nkt; ++kt) {
+                    c += tcost(qt, kt);
+                    // close the piece at cost T if the next one may start at kt + 1
+                    if (c >= T && kt + 1 < nkt && kt + 1 <= kdiag && np + 1 < MAXP) {
+                        cut[qt][++np] = kt + 1;
+                        c = START;
+                    }
+                }
+                cut[qt][++np] = nkt;
+                npc[qt] = np;
+            }
+            if (fits()) break;
+        }
     }
-    // items longest first (ties: later block first), slots in block order
-    struct It { int size, qt, part; };
+    // items: block order from the last block down, then stable-sorted by cost
+    struct It { float cost; int qt, lo, hi, slot; };
     It list[PF_MAX_ITEMS];
     int n = 0, slot = 0;
     for (int qt = nq - 1; qt >= 0; --qt) {
-        int np, per;
-        pf_parts(qt, m, P, L, np, per);
-        const int nkt = pf_nkt(qt, m, P);
+        const int np = npc[qt];
         wk.slot0[qt] = (int16_t) (np > 1 ? slot : -1);
-        if (np > 1) { wk.split_qt[wk.n_split++] = (uint8_t) qt; slot += np; }
+        wk.nparts[qt] = (uint8_t) np;
+        if (np > 1) wk.split_qt[wk.n_split++] = (uint8_t) qt;
         for (int p = 0; p < np; ++p) {
-            const int k0 = p * per, k1 = (k0 + per < nkt) ? k0 + per : nkt;
-            list[n++] = It{ k1 - k0, qt, p };
+            float c = START;
+            for (int kt = cut[qt][p]; kt < cut[qt][p + 1]; ++kt) c += tcost(qt, kt);
+            list[n++] = It{ c, qt, cut[qt][p], cut[qt][p + 1], np > 1 ? slot + p : -1 };
         }
+        if (np > 1) slot += np;
     }
-    std::stable_sort(list, list + n, [](const It & a, const It & b) { return a.size > b.size; });
-    for (int i = 0; i < n; ++i) wk.item[i] = (uint16_t) (list[i].qt | (list[i].part << 8));
+    if (wk.n_split == 0) { wk.n_items = 0; return; }
+    std::stable_sort(list, list + n, [](const It & a, const It & b) { return a.cost > b.cost; });
+    for (int i = 0; i < n; ++i) {
+        wk.item[i] = (uint32_t) list[i].qt | ((uint32_t) (list[i].slot + 1) << 16);
+        wk.krange[i] = (uint32_t) list[i].lo | ((uint32_t) list[i].hi << 16);
+    }
     wk.n_items = n;
-    wk.lsplit = L;
 }
 
 template <bool INT8>
@@ -932,7 +1002,7 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
                           const _Float16 * kc, const _Float16 * vc, int near, int sink, float * o,
                           int8_t * aqs, float2 * asc, hipStream_t st, const char * what) {
     PfWork wk;
-    pf_plan(m, P, wk);
+    pf_plan(m, P, near, sink, INT8, wk);
     if (wk.n_items == 0) {
         hipLaunchKernelGGL(lk_k_pf_attn<INT8>, dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0, st,
                            q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk,
