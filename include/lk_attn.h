@@ -284,6 +284,15 @@ int lk_pf_ctx_buffers(const lk_pf_ctx * ctx, int layer, void ** qh, int8_t ** k8
 int lk_pf_qk_i32(const int8_t * q8, int m, const int8_t * k8, int n,
                  int32_t * s, void * stream);
 
+/* The split work list lk_pf_attn8 (int8 != 0) or lk_pf_attn would launch for
+ * a chunk (m, P, near, sink), under the current lk_pf_split_override and for
+ * the current device's slot count (512 when no device is visible): items in
+ * dispatch order as int32 quadruples (query block, first key tile, end key
+ * tile, partial slot or -1) into items[4 * max_items].  Returns the item count
+ * (0: an unsplit launch), or -1 on bad arguments.  Host-side only, no device
+ * work; no counterpart in the reference (its kernels do not split). */
+int lk_pf_plan_items(int m, int P, int near, int sink, int int8, int32_t * items, int max_items);
+
 #ifdef __cplusplus
 }
 #endif

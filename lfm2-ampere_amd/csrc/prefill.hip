@@ -996,6 +996,19 @@ static void pf_plan(int m, int P, int near, int sink, bool int8, PfWork & wk) {
     wk.n_items = n;
 }
 
+extern "C" int lk_pf_plan_items(int m, int P, int near, int sink, int int8, int32_t * items, int max_items) {
+    if (m < 1 || P < 0 || max_items < 0 || (!items && max_items > 0)) return -1;
+    PfWork wk;
+    pf_plan(m, P, near, sink, int8 != 0, wk);
+    for (int i = 0; i < wk.n_items && i < max_items; ++i) {
+        items[4 * i + 0] = (int32_t) (wk.item[i] & 255);
+        items[4 * i + 1] = (int32_t) (wk.krange[i] & 0xffff);
+        items[4 * i + 2] = (int32_t) (wk.krange[i] >> 16);
+        items[4 * i + 3] = (int32_t) (wk.item[i] >> 16) - 1;
+    }
+    return wk.n_items;
+}
+
 template <bool INT8>
 static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qcs, const _Float16 * qh,
                           int m, int P, const int8_t * k8, const float * ksc, int kstride,

@@ -29,7 +29,7 @@ EXPORTS = (
     "lk_decode_graph_create", "lk_decode_graph_launch", "lk_decode_graph_nodes",
     "lk_decode_graph_destroy",
     "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_split_override",
-    "lk_pf_qk_i32", "lk_qk_norm_rope", "lk_pf_qknr",
+    "lk_pf_qk_i32", "lk_pf_plan_items", "lk_qk_norm_rope", "lk_pf_qknr",
     "lk_decode_step_graph_create", "lk_decode_graph_run",
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
     "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows",
@@ -77,6 +77,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_attn": ([P, I, I, P, P, P, P], I),
         "lk_pf_split_override": ([I], I),
         "lk_pf_qk_i32": ([P, I, P, I, P, P], I),
+        "lk_pf_plan_items": ([I, I, I, I, I, P, I], I),
         "lk_qk_norm_rope": ([P, P, P, P, P, P, P, P, P], I),
         "lk_pf_qknr": ([P, P, P, I, I, P, P, P, P, P, I, P, P], I),
         "lk_decode_step_graph_create": ([I, P, P, P, P, P], I),
@@ -300,6 +301,19 @@ def pf_quant_rows(X, rows, ld, kb, qs, sc, stream=None) -> None:
 def pf_split_override(tiles: int) -> None:
     """-1 never split prefill blocks, 0 automatic, n > 0 parts of <= n key tiles."""
     _check(load().lk_pf_split_override(int(tiles)), "lk_pf_split_override")
+
+
+def pf_plan_items(m: int, P: int, near: int, sink: int, int8: bool = True, max_items: int = 1024):
+    """The split work list of a prefill chunk, in dispatch order: a list of
+    (query block, first key tile, end key tile, partial slot or -1); [] for an
+    unsplit launch.  Host-side only."""
+    import ctypes
+    buf = (ctypes.c_int32 * (4 * max_items))()
+    n = load().lk_pf_plan_items(int(m), int(P), int(near), int(sink), int(bool(int8)),
+                                ctypes.addressof(buf), int(max_items))
+    if n < 0:
+        raise LkError("lk_pf_plan_items: bad arguments")
+    return [tuple(buf[4 * i:4 * i + 4]) for i in range(min(n, max_items))]
 
 
 def pf_qk_i32(q8, m, k8, n, s, stream=None) -> None:

@@ -33,3 +33,11 @@ def lk():
     assert torch.cuda.is_available(), "gpu tests need a GPU"
     lk_attn.load()
     return lk_attn
+
+
+@pytest.fixture(scope="session")
+def lk_host():
+    """The HIP library for host-side entry points (no device needed)."""
+    import lk_attn
+    lk_attn.load()
+    return lk_attn
