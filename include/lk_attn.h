@@ -123,7 +123,9 @@ int lk_decode_graph_destroy(lk_decode_graph * graph);
  * q/k/v projection rows (q_src, k_src, v_src fp32, the projection GEMV's
  * output) into the working q / k buffers with K/V appended at row *d_pos of the
  * layer's cache (lk_qk_norm_rope's arithmetic, out of place), split and
- * combine; then *d_pos += 1.
+ * combine; then *d_pos += 1.  The producer runs inside the split kernel (each
+ * workgroup forms q itself; the one whose slice holds *d_pos appends K/V and
+ * uses the new row directly), so a layer is two graph nodes.
  * Replaying it n times runs n decode steps with no host work in between.
  * All pointers are device pointers owned by the caller; `part` is shared by
  * the layers. */

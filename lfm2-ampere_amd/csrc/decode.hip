@@ -53,10 +53,50 @@ __device__ __forceinline__ void lk_split_h(float x, _Float16 & hi, _Float16 & lo
 #define LK_DEC_ABLATE 0
 #endif
 
+// The decode producer (reference k_qk_norm_rope, kernels.cu:871-915) folded
+// into the split kernel for the step graph: the inputs of one head row in the
+// split kernel's q layout -- lane (col, g) holds dims 8g+i ("lo") and
+// 32+8g+i ("hi"), i < 8, of the row, replicated over the columns -- normalised
+// and rotated with the arithmetic of lk_k_qk_norm_rope bit for bit: squares
+// rounded, the sum tree over d with strides 32 (in lane), 16 and 8 (lanes
+// ^32, ^16: lk_xrow_sum adds in that order, both partners the same two
+// values), then 4, 2, 1 in lane; 1/sqrt in fp64 rounded once; the rotation of
+// the pair (d, d+32) with the table entry d.
+__device__ __forceinline__ void lk_norm_rope_pair8(float (&lo)[8], float (&hi)[8], const float * __restrict__ wn,
+                                                   int g, const float * s_c, const float * s_s) {
+#pragma clang fp contract(off)
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float a = lo[i] * lo[i], b = hi[i] * hi[i];
+        t[i] = lk_xrow_sum(a + b);
+    }
+    const float u0 = t[0] + t[4], u1 = t[1] + t[5], u2 = t[2] + t[6], u3 = t[3] + t[7];
+    const float ss = (u0 + u2) + (u1 + u3);
+    const float arg = ss * (1.0f / LK_HEAD_DIM) + LK_EPS_F;
+    const float inv = (float) (1.0 / sqrt((double) arg));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int d = 8 * g + i;
+        const float yl = (lo[i] * inv) * wn[d], yh = (hi[i] * inv) * wn[32 + d];
+        const float c = s_c[d], sn = s_s[d];
+        lo[i] = yl * c - yh * sn;
+        hi[i] = yl * sn + yh * c;
+    }
+}
+// Pointers of the folded producer: projection rows in, working q / k rows out
+// (the in-place API's buffers), norm weights; the cache row at *d_pos is
+// written by the workgroup whose slice holds it.
+struct LkDecProducer {
+    const float * q_src, * k_src, * v_src, * q_norm, * k_norm;
+    float * q_out, * k_out;
+};
+
+template <bool FUSED>
 __global__ void __launch_bounds__(LK_DEC_THREADS)
-lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
-                const _Float16 * __restrict__ vc, const int * __restrict__ d_pos,
-                float * __restrict__ part) {
+lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
+                const _Float16 * vc, const int * __restrict__ d_pos,
+                float * __restrict__ part, const LkDecProducer pr) {
     constexpr int RPW = 2 * LK_DEC_TILE / 8;                   // rows fetched per wave per tile
     constexpr int NG  = LK_DEC_TILE / 16;                      // 16-token groups per tile
     constexpr int D   = LK_DEC_NBUF - 1;                       // tiles in flight
@@ -121,6 +161,40 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
     for (int i = 0; i < D; ++i)
         if (i < ntile) fetch(i);
 
+    // Folded producer: the 32 (cos, sin) entries of position seq-1, 4 per wave.
+    __shared__ float s_c[FUSED ? LK_HEAD_DIM / 2 : 1], s_s[FUSED ? LK_HEAD_DIM / 2 : 1];
+    const int pos = seq - 1;
+    const bool own_pos = FUSED && t1 == seq;               // this slice holds position pos
+    lk_h8 kv_h[4];                                         // its K lo, K hi, V lo, V hi (fp16)
+    if constexpr (FUSED) {
+        if (lane < 4) lk_rope_entry(pos, 4 * w + lane, s_c[4 * w + lane], s_s[4 * w + lane]);
+        __syncthreads();
+        if (own_pos) {
+            float lo[8], hi[8];
+            const float * kp = pr.k_src + w * LK_HEAD_DIM + 8 * g;
+            const float * vp = pr.v_src + w * LK_HEAD_DIM + 8 * g;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { lo[i] = kp[i]; hi[i] = kp[32 + i]; }
+            lk_norm_rope_pair8(lo, hi, pr.k_norm, g, s_c, s_s);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                kv_h[0][i] = (_Float16) lo[i]; kv_h[1][i] = (_Float16) hi[i];
+                kv_h[2][i] = (_Float16) vp[i]; kv_h[3][i] = (_Float16) vp[32 + i];
+            }
+            if (col == 0) {
+                const size_t off = ((size_t) pos * LK_N_KV_HEADS + w) * LK_HEAD_DIM + 8 * g;
+                _Float16 * kw = (_Float16 *) kc, * vw = (_Float16 *) vc;
+                *(lk_h8 *) (kw + off) = kv_h[0]; *(lk_h8 *) (kw + off + 32) = kv_h[1];
+                *(lk_h8 *) (vw + off) = kv_h[2]; *(lk_h8 *) (vw + off + 32) = kv_h[3];
+                float * ko = pr.k_out + w * LK_HEAD_DIM + 8 * g;
+                *(lk_f4 *) ko        = (lk_f4){ lo[0], lo[1], lo[2], lo[3] };
+                *(lk_f4 *) (ko + 4)  = (lk_f4){ lo[4], lo[5], lo[6], lo[7] };
+                *(lk_f4 *) (ko + 32) = (lk_f4){ hi[0], hi[1], hi[2], hi[3] };
+                *(lk_f4 *) (ko + 36) = (lk_f4){ hi[4], hi[5], hi[6], hi[7] };
+            }
+        }
+    }
+
     // Scores are computed transposed, S^T = K . Q^T (v_mfma_f32_16x16x32_f16):
     // A = 16 cache rows of the tile (lane: position col, dims 32ks+8g..+7),
     // B = Q^T with the 4 heads of kv head w replicated over the 16 columns
@@ -130,15 +204,27 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
     // and both halves are multiplied.
     lk_h8 qbh[2], qbl[2];
     {
-        const float * qp = q + (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
+        const int qrow = (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
+        const float * qp = (FUSED ? pr.q_src : q) + qrow;
+        float lo[8], hi[8];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                _Float16 h, l;
-                lk_split_h(qp[32 * ks + i], h, l);
-                qbh[ks][i] = h; qbl[ks][i] = l;
+        for (int i = 0; i < 8; ++i) { lo[i] = qp[i]; hi[i] = qp[32 + i]; }
+        if constexpr (FUSED) {
+            lk_norm_rope_pair8(lo, hi, pr.q_norm, g, s_c, s_s);
+            if (sp == 0 && col < 4) {                       // the working q, once
+                float * qo = pr.q_out + qrow;
+                *(lk_f4 *) qo        = (lk_f4){ lo[0], lo[1], lo[2], lo[3] };
+                *(lk_f4 *) (qo + 4)  = (lk_f4){ lo[4], lo[5], lo[6], lo[7] };
+                *(lk_f4 *) (qo + 32) = (lk_f4){ hi[0], hi[1], hi[2], hi[3] };
+                *(lk_f4 *) (qo + 36) = (lk_f4){ hi[4], hi[5], hi[6], hi[7] };
             }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            _Float16 h, l;
+            lk_split_h(lo[i], h, l); qbh[0][i] = h; qbl[0][i] = l;
+            lk_split_h(hi[i], h, l); qbh[1][i] = h; qbl[1][i] = l;
+        }
     }
     const float SC = 0.125f * LK_LOG2E_F;      // scores in log2 units
     // Running max is raised only when a score exceeds it by 2^8 in p: P stays
@@ -223,6 +309,16 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * __restrict__ kc,
 
     for (int it = 0; it < ntile; ++it) {
         wait_tile(it);
+        if (own_pos && it == ntile - 1 && col == 0) {
+            // the new row, as the cache now holds it (the tile's copy may predate
+            // the store above); wave w alone reads kv head w's bytes of a row
+            const int rt = pos - t0 - it * LK_DEC_TILE;
+            unsigned char * b = s_tile[it % LK_DEC_NBUF] + w * 128 + 16 * g;
+            *(lk_h8 *) (b + rt * LK_DEC_ROWB) = kv_h[0];
+            *(lk_h8 *) (b + rt * LK_DEC_ROWB + 64) = kv_h[1];
+            *(lk_h8 *) (b + (LK_DEC_TILE + rt) * LK_DEC_ROWB) = kv_h[2];
+            *(lk_h8 *) (b + (LK_DEC_TILE + rt) * LK_DEC_ROWB + 64) = kv_h[3];
+        }
         consume(s_tile[it % LK_DEC_NBUF], it);
         // every wave is done reading buffer it % NBUF before it is refilled
         __builtin_amdgcn_s_barrier();
@@ -282,19 +378,6 @@ __device__ __forceinline__ void lk_quant_q8_1_half(float x, lk_block_q8_1 * __re
     }
 }
 
-// Sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the gfx950
-// lane swaps; like lk_xrow_max, every lane ends with identical bits.
-#ifdef __HIP_DEVICE_COMPILE__
-__device__ __forceinline__ float lk_xrow_sum(float x) {
-    float a = x, b = x;
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-    float c = a + b, d = c;
-    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
-    return c + d;
-}
-#else
-__device__ __forceinline__ float lk_xrow_sum(float x) { return x; }
-#endif
 
 // Combine: grid (32 query heads, 2 halves of the 64 dims), 256 threads;
 // workgroup (head, half) produces 32 output dims, wave w owns dims
@@ -427,9 +510,16 @@ lk_k_attention_decode(const float * __restrict__ q, const _Float16 * __restrict_
 // C ABI
 static int lk_split_launch(const float * q, const void * kc, const void * vc,
                            const int * d_pos, float * part, hipStream_t st) {
-    hipLaunchKernelGGL(lk_k_attn_split, dim3(LK_ATTN_SPLIT), dim3(LK_DEC_THREADS), 0, st,
-                       q, (const _Float16 *) kc, (const _Float16 *) vc, d_pos, part);
+    hipLaunchKernelGGL(lk_k_attn_split<false>, dim3(LK_ATTN_SPLIT), dim3(LK_DEC_THREADS), 0, st,
+                       q, (const _Float16 *) kc, (const _Float16 *) vc, d_pos, part, LkDecProducer{});
     return lk_launch_status("lk_attn_split");
+}
+// The step graph's attention node: the split kernel with the producer folded in.
+static int lk_split_fused_launch(const lk_decode_layer & L, const int * d_pos, float * part, hipStream_t st) {
+    const LkDecProducer pr{ L.q_src, L.k_src, L.v_src, L.q_norm, L.k_norm, L.q, L.k };
+    hipLaunchKernelGGL(lk_k_attn_split<true>, dim3(LK_ATTN_SPLIT), dim3(LK_DEC_THREADS), 0, st,
+                       (const float *) nullptr, (const _Float16 *) L.kc, (const _Float16 *) L.vc, d_pos, part, pr);
+    return lk_launch_status("lk_decode_step_graph (split with producer)");
 }
 static int lk_combine_launch(const float * part, const int * d_pos, float * out,
                              lk_block_q8_1 * yq8, hipStream_t st) {
@@ -542,11 +632,9 @@ extern "C" int lk_decode_step_graph_create(int n_layers, const lk_decode_layer *
     int rc = 0;
     for (int i = 0; i < n_layers && !rc; ++i) {
         const lk_decode_layer & L = layers[i];
-        // the producer reads the projection rows and writes the working q / k
-        // (the in-place API's arithmetic, out of place)
-        rc = lk_qknr_decode_launch(L.q_src, L.k_src, L.q, L.k, L.v_src, L.q_norm, L.k_norm, d_pos,
-                                   L.kc, L.vc, st);
-        if (!rc) rc = lk_split_launch(L.q, L.kc, L.vc, d_pos, part, st);
+        // the producer (norm + RoPE of q and k, the cache append, the working
+        // q / k rows) runs inside the split kernel: two nodes per layer
+        rc = lk_split_fused_launch(L, d_pos, part, st);
         if (!rc) rc = lk_combine_launch(part, d_pos, L.out, L.yq8, st);
     }
     if (!rc) {

@@ -98,6 +98,20 @@ __device__ __forceinline__ float lk_xrow_max(float x) {
 __device__ __forceinline__ float lk_xrow_max(float x) { return x; }
 #endif
 
+// Sum over the four 16-lane rows (lanes l, l^16, l^32, l^48) with the gfx950
+// lane swaps; like lk_xrow_max, every lane ends with identical bits.
+#ifdef __HIP_DEVICE_COMPILE__
+__device__ __forceinline__ float lk_xrow_sum(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    float c = a + b, d = c;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
+    return c + d;
+}
+#else
+__device__ __forceinline__ float lk_xrow_sum(float x) { return x; }
+#endif
+
 // Four fp16 of one column from a row-major LDS tile via the gfx950 transpose
 // read (ds_read_b64_tr_b16).  Within each 16-lane group, lane 4a+b supplies
 // the address of T[row0 + a][col0 + 4b .. +3]; lane c then receives
@@ -128,6 +142,19 @@ __host__ __device__ __forceinline__ void lk_attn_slices(int seq, int & ns, int &
     if (s > LK_ATTN_SPLIT)     s = LK_ATTN_SPLIT;
     ns = s;
     chunk = (seq + s - 1) / s;
+}
+
+// ---- rotary embedding constants and table entry (qknr.hip, decode.hip) -----------
+// Reference kernels.cuh:22-24: LK_EPS 1e-5, LK_ROPE_THETA 1e7.  Entry i < 32 of
+// position pos: f = theta^(-i/32) and the cosine and sine of the fp32 angle
+// (float) pos * f, each evaluated in fp64 and rounded once to fp32.
+#define LK_EPS_F        1e-5f
+#define LK_ROPE_THETA_D 10000000.0
+__device__ __forceinline__ void lk_rope_entry(int pos, int i, float & c, float & s) {
+    const float f = (float) pow(LK_ROPE_THETA_D, -(double) i / 32.0);
+    const float a = (float) pos * f;                           // fp32 product, as the reference
+    c = (float) cos((double) a);
+    s = (float) sin((double) a);
 }
 
 // ---- int8 row quantiser on 8-lane groups (shared by prefill.hip, qknr.hip) -----

@@ -32,20 +32,13 @@
 #include "lk_common.h"
 #include <math.h>
 
-#define LK_EPS_F        1e-5f
-#define LK_ROPE_THETA_D 10000000.0
 #define LK_QKNR_ROWS    (LK_N_HEADS + LK_N_KV_HEADS)   // 40 groups per token
 #define LK_QKNR_THREADS (LK_QKNR_ROWS * 8)              // 320
 
 // (cos, sin) of the 32 rotary angles of position pos, into LDS (threads 0..31).
 __device__ __forceinline__ void lk_rope_table(int pos, float * s_c, float * s_s) {
     const int i = threadIdx.x;
-    if (i < LK_HEAD_DIM / 2) {
-        const float f = (float) pow(LK_ROPE_THETA_D, -(double) i / 32.0);
-        const float a = (float) pos * f;                       // fp32 product, as the reference
-        s_c[i] = (float) cos((double) a);
-        s_s[i] = (float) sin((double) a);
-    }
+    if (i < LK_HEAD_DIM / 2) lk_rope_entry(pos, i, s_c[i], s_s[i]);
 }
 
 // Norm + rotation of one 64-wide row held by an 8-lane group (lane j: values

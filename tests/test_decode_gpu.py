@@ -232,8 +232,8 @@ def test_config_c3_graph(lk, oracle):
 
 
 def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
-    """The decode step graph (per layer: qk norm + RoPE + cache append, split,
-    combine; then d_pos += 1) replayed n times = n decode steps: cache
+    """The decode step graph (per layer: qk norm + RoPE + cache append folded
+    into the split, combine; then d_pos += 1) replayed n times = n decode steps: cache
     rows, d_pos and every layer's output against the oracle, and the replay
     bit-identical to the same kernels called eagerly."""
     rng = np.random.default_rng(61)
@@ -259,7 +259,7 @@ def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
     d_pos = torch.tensor([P0], dtype=torch.int32, device="cuda")
     part = torch.empty(lk.part_bytes() // 4, device="cuda")
     g = lk.DecodeStepGraph(Ls, d_pos, part)
-    assert g.nodes() == 3 * layers + 1
+    assert g.nodes() == 2 * layers + 1       # producer folded into the split node
     g.run(steps)
     g.stream.synchronize()
     assert int(d_pos.item()) == P0 + steps
@@ -280,6 +280,10 @@ def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
         assert torch.equal(L["out"].view(torch.int32), M["out"].view(torch.int32))
         assert torch.equal(L["yq8"], M["yq8"])
         assert torch.equal(L["kc"].view(torch.int16), M["kc"].view(torch.int16))
+        assert torch.equal(L["vc"].view(torch.int16), M["vc"].view(torch.int16))
+        # the working q / k rows of the last step, as the standalone producer writes them
+        assert torch.equal(L["q"].view(torch.int32), M["q"].view(torch.int32))
+        assert torch.equal(L["k"].view(torch.int32), M["k"].view(torch.int32))
     # against the oracle: appended rows and the last step's output
     last = P0 + steps - 1
     for (qs, ks, vs, qn, kn, kc0, vc0), L in zip(host_in, Ls):
