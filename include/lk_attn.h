@@ -117,7 +117,7 @@ int lk_decode_graph_destroy(lk_decode_graph * graph);
 
 /* ---- decode step graph -----------------------------------------------------
  * The engine captures its whole position-independent decode step once and
- * replays it, the last kernel advancing d_pos on the device (reference
+ * replays it, its last kernel advancing d_pos on the device (reference
  * engine.cu:1328-1342 capture, 1750-1760 replay loop, kernels.cu:994 advance).
  * This is that step's attention slice: per layer, the q/k norm + RoPE of the
  * q/k/v projection rows (q_src, k_src, v_src fp32, the projection GEMV's
@@ -125,7 +125,8 @@ int lk_decode_graph_destroy(lk_decode_graph * graph);
  * layer's cache (lk_qk_norm_rope's arithmetic, out of place), split and
  * combine; then *d_pos += 1.  The producer runs inside the split kernel (each
  * workgroup forms q itself; the one whose slice holds *d_pos appends K/V and
- * uses the new row directly), so a layer is two graph nodes.
+ * uses the new row directly), so a layer is two graph nodes; the last
+ * layer's combine advances *d_pos.
  * Replaying it n times runs n decode steps with no host work in between.
  * All pointers are device pointers owned by the caller; `part` is shared by
  * the layers. */

@@ -393,8 +393,11 @@ __device__ __forceinline__ void lk_quant_q8_1_half(float x, lk_block_q8_1 * __re
 static_assert(LK_ATTN_SPLIT <= 256 && LK_ATTN_SPLIT % 64 == 0, "combine: 1-4 whole slots per lane");
 __global__ void __launch_bounds__(256)
 lk_k_attn_combine(const float * __restrict__ part, const int * __restrict__ d_pos,
-                  float * __restrict__ out, lk_block_q8_1 * __restrict__ yq8) {
+                  float * __restrict__ out, lk_block_q8_1 * __restrict__ yq8, int * __restrict__ advance) {
     (void) d_pos;
+    // the decode step's position advance (reference kernels.cu:994), folded
+    // into the step's last combine: nothing in this kernel reads the position
+    if (advance && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *advance = *advance + 1;
     constexpr int J = LK_ATTN_SPLIT / 64;
     const int head = blockIdx.x, half = blockIdx.y;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -522,8 +525,8 @@ static int lk_split_fused_launch(const lk_decode_layer & L, const int * d_pos, f
     return lk_launch_status("lk_decode_step_graph (split with producer)");
 }
 static int lk_combine_launch(const float * part, const int * d_pos, float * out,
-                             lk_block_q8_1 * yq8, hipStream_t st) {
-    hipLaunchKernelGGL(lk_k_attn_combine, dim3(LK_N_HEADS, 2), dim3(256), 0, st, part, d_pos, out, yq8);
+                             lk_block_q8_1 * yq8, hipStream_t st, int * advance = nullptr) {
+    hipLaunchKernelGGL(lk_k_attn_combine, dim3(LK_N_HEADS, 2), dim3(256), 0, st, part, d_pos, out, yq8, advance);
     return lk_launch_status("lk_attn_combine");
 }
 
@@ -608,11 +611,6 @@ extern "C" int lk_decode_graph_create(int n_layers, const float * const * q,
     return 0;
 }
 
-// The step's last node: the position advance (reference kernels.cu:994).
-__global__ void lk_k_advance_pos(int * __restrict__ d_pos) {
-    if (threadIdx.x == 0) *d_pos = *d_pos + 1;
-}
-
 extern "C" int lk_decode_step_graph_create(int n_layers, const lk_decode_layer * layers, int * d_pos,
                                            float * part, void * stream, lk_decode_graph ** graph) {
     if (!graph) return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: graph is null");
@@ -635,11 +633,8 @@ extern "C" int lk_decode_step_graph_create(int n_layers, const lk_decode_layer *
         // the producer (norm + RoPE of q and k, the cache append, the working
         // q / k rows) runs inside the split kernel: two nodes per layer
         rc = lk_split_fused_launch(L, d_pos, part, st);
-        if (!rc) rc = lk_combine_launch(part, d_pos, L.out, L.yq8, st);
-    }
-    if (!rc) {
-        hipLaunchKernelGGL(lk_k_advance_pos, dim3(1), dim3(64), 0, st, d_pos);
-        rc = lk_launch_status("lk_decode_step_graph_create");
+        // the last layer's combine also advances *d_pos
+        if (!rc) rc = lk_combine_launch(part, d_pos, L.out, L.yq8, st, i == n_layers - 1 ? d_pos : nullptr);
     }
     hipGraph_t g = nullptr;
     e = hipStreamEndCapture(st, &g);

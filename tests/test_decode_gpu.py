@@ -233,7 +233,8 @@ def test_config_c3_graph(lk, oracle):
 
 def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
     """The decode step graph (per layer: qk norm + RoPE + cache append folded
-    into the split, combine; then d_pos += 1) replayed n times = n decode steps: cache
+    into the split, combine; d_pos += 1 in the last combine) replayed n times =
+    n decode steps: cache
     rows, d_pos and every layer's output against the oracle, and the replay
     bit-identical to the same kernels called eagerly."""
     rng = np.random.default_rng(61)
@@ -259,7 +260,7 @@ def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
     d_pos = torch.tensor([P0], dtype=torch.int32, device="cuda")
     part = torch.empty(lk.part_bytes() // 4, device="cuda")
     g = lk.DecodeStepGraph(Ls, d_pos, part)
-    assert g.nodes() == 2 * layers + 1       # producer folded into the split node
+    assert g.nodes() == 2 * layers           # producer in the split node, advance in the last combine
     g.run(steps)
     g.stream.synchronize()
     assert int(d_pos.item()) == P0 + steps
