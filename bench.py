@@ -251,6 +251,32 @@ def bench_prefill_c5(lk, lkc, reps):
     }
 
 
+def bench_read_reference(lk, bytes_list=(67108864, 268435456), nbuf=10, iters=20):
+    """The practical HBM read rate of this GPU, for scale: the library's plain
+    streaming-read probe (lk_read_probe) over buffers of the decode layers'
+    sizes (C2 67 MB, C3 268 MB), cycling over nbuf distinct buffers so that the
+    256 MB last-level cache does not serve them.  The split kernel's rate is
+    best read against this, the datasheet 8 TB/s not being reachable by reads."""
+    import torch
+    out = {}
+    sink = torch.zeros(1, device="cuda")
+    for nb in bytes_list:
+        bufs = [torch.ones(nb // 4, device="cuda") for _ in range(nbuf)]
+        for b in bufs[:2]:
+            lk.read_probe(b, sink)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(iters):
+            lk.read_probe(bufs[i % nbuf], sink)
+        e1.record(); e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        out[f"{nb >> 20}MiB"] = {"us": us, "GBps": nb / (us * 1e-6) / 1e9}
+        del bufs
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_producers(lk, iters):
     """The attention-input producers (reference kernels.cu:871-915,
     prefill.cu:975-1016): the prefill pass over one 4096-token chunk (C4's
@@ -481,6 +507,9 @@ def main():
     c3 = bench_decode(lk, lkc, "C3", max(20, args.steps // 4), max(3, args.warmup // 4), args.kernel_iters // 2)
     log(json.dumps(c3))
     results = {"C2_decode_32k": c2, "C3_decode_131k": c3}
+    log("practical HBM read rate (plain streaming read of the decode layer sizes)")
+    results["hbm_read_reference"] = bench_read_reference(lk)
+    log(json.dumps(results["hbm_read_reference"]))
     log("decode step graph (producer + attention, 10 layers, 32k context)")
     results["C2_decode_step_graph"] = bench_decode_step(lk, 50, 10)
     log(json.dumps(results["C2_decode_step_graph"]))

@@ -296,6 +296,13 @@ int lk_pf_qk_i32(const int8_t * q8, int m, const int8_t * k8, int n,
  * work; no counterpart in the reference (its kernels do not split). */
 int lk_pf_plan_items(int m, int P, int near, int sink, int int8, int32_t * items, int max_items);
 
+/* Measurement reference, not on the attention path: a plain streaming read of
+ * `bytes` (a multiple of 16, 16-byte aligned) at `src`, for the practical HBM
+ * read rate next to the decode kernels' (the datasheet peak is not reachable
+ * by reads).  `sink`: one fp32, written only under a condition the data never
+ * meets.  No counterpart in the reference. */
+int lk_read_probe(const void * src, size_t bytes, float * sink, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,7 +29,7 @@ EXPORTS = (
     "lk_decode_graph_create", "lk_decode_graph_launch", "lk_decode_graph_nodes",
     "lk_decode_graph_destroy",
     "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_split_override",
-    "lk_pf_qk_i32", "lk_pf_plan_items", "lk_qk_norm_rope", "lk_pf_qknr",
+    "lk_pf_qk_i32", "lk_pf_plan_items", "lk_read_probe", "lk_qk_norm_rope", "lk_pf_qknr",
     "lk_decode_step_graph_create", "lk_decode_graph_run",
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
     "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows",
@@ -78,6 +78,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_split_override": ([I], I),
         "lk_pf_qk_i32": ([P, I, P, I, P, P], I),
         "lk_pf_plan_items": ([I, I, I, I, I, P, I], I),
+        "lk_read_probe": ([P, S, P, P], I),
         "lk_qk_norm_rope": ([P, P, P, P, P, P, P, P, P], I),
         "lk_pf_qknr": ([P, P, P, I, I, P, P, P, P, P, I, P, P], I),
         "lk_decode_step_graph_create": ([I, P, P, P, P, P], I),
@@ -301,6 +302,12 @@ def pf_quant_rows(X, rows, ld, kb, qs, sc, stream=None) -> None:
 def pf_split_override(tiles: int) -> None:
     """-1 never split prefill blocks, 0 automatic, n > 0 parts of <= n key tiles."""
     _check(load().lk_pf_split_override(int(tiles)), "lk_pf_split_override")
+
+
+def read_probe(buf, sink, stream=None) -> None:
+    """Plain streaming read of a device tensor (measurement reference)."""
+    _check(load().lk_read_probe(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
+                                _stream(stream)), "lk_read_probe")
 
 
 def pf_plan_items(m: int, P: int, near: int, sink: int, int8: bool = True, max_items: int = 1024):

@@ -299,3 +299,16 @@ def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
         ref = oracle.decode_ref(q_rot.reshape(32, 64), kc_h[:last + 1].reshape(-1), vc_h[:last + 1].reshape(-1), last + 1)
         assert oracle.rel_err(host(L["out"]), ref) <= 2e-3
     g.close()
+
+
+def test_read_probe_reads_and_leaves_sink(lk):
+    """The measurement probe (not on the attention path) runs over a buffer and
+    leaves its sink untouched; misaligned sizes are rejected."""
+    buf = torch.ones(1 << 20, device="cuda")
+    sink = torch.zeros(1, device="cuda")
+    note("read probe")
+    lk.read_probe(buf, sink)
+    torch.cuda.synchronize()
+    assert float(sink.item()) == 0.0
+    with pytest.raises(Exception):
+        lk.read_probe(torch.ones(3, dtype=torch.float16, device="cuda"), sink)
