@@ -225,12 +225,6 @@ __device__ __forceinline__ void lk_wait_vm() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-// ---- launchers shared between translation units -------------------------------
-// qs/ks -> qf/kf (may alias: in place)
-int lk_qknr_decode_launch(const float * qs, const float * ks, float * qf, float * kf, const float * vf,
-                          const float * qn, const float * kn, const int * d_pos, void * kc, void * vc,
-                          hipStream_t st);
-
 // ---- host-side error plumbing (lk_host.cpp) -----------------------------------
 int lk_fail(int code, const char * fmt, ...);
 // hipGetLastError after a launch, mapped into lk_fail.

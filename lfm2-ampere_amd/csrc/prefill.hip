@@ -183,8 +183,8 @@ __host__ __device__ inline int pf_nkt(int qt, int m, int P) {
     const int qlast = (qt * PF_BQ + PF_BQ < m) ? qt * PF_BQ + PF_BQ : m;
     return (P + qlast + PF_BK - 1) / PF_BK;
 }
-// Equal-size parts of at most lsplit tiles (the test hook's plan).
-__host__ __device__ inline void pf_parts(int qt, int m, int P, int lsplit, int & np, int & per) {
+// Equal-size parts of at most lsplit tiles (the test hook's plan; host only).
+static inline void pf_parts(int qt, int m, int P, int lsplit, int & np, int & per) {
     const int nkt = pf_nkt(qt, m, P);
     np = (lsplit > 0) ? (nkt + lsplit - 1) / lsplit : 1;
     if (np < 1) np = 1;

@@ -160,9 +160,10 @@ lk_k_pf_qknr(const float * __restrict__ Y, const float * __restrict__ qn, const 
 
 // ---------------------------------------------------------------------------
 // C ABI
-int lk_qknr_decode_launch(const float * qs, const float * ks, float * qf, float * kf, const float * vf,
-                          const float * qn, const float * kn, const int * d_pos, void * kc, void * vc,
-                          hipStream_t st) {
+// qs/ks -> qf/kf (may alias: in place)
+static int lk_qknr_decode_launch(const float * qs, const float * ks, float * qf, float * kf, const float * vf,
+                                 const float * qn, const float * kn, const int * d_pos, void * kc, void * vc,
+                                 hipStream_t st) {
     hipLaunchKernelGGL(lk_k_qk_norm_rope, dim3(1), dim3(LK_QKNR_THREADS), 0, st,
                        qs, ks, qf, kf, vf, qn, kn, d_pos, (_Float16 *) kc, (_Float16 *) vc);
     return lk_launch_status("lk_qk_norm_rope");
