@@ -226,6 +226,38 @@ def test_attn_split_parts(lk, oracle, m, P, near, L):
     assert np.array_equal(again8.view(np.uint32), part8.view(np.uint32))
 
 
+# ---- the automatic (cost-model) split plan ------------------------------------------------------
+AUTO_CASES = [(1000, 0, 256), (777, 0, 1024), (1500, 300, 96), (2048, 777, 1024), (4096, 4096, 1024)]
+
+
+@pytest.mark.parametrize("m,P,near", AUTO_CASES, ids=[f"m{c[0]}_P{c[1]}_n{c[2]}" for c in AUTO_CASES])
+def test_attn_auto_split(lk, oracle, m, P, near):
+    """Chunks the automatic plan cuts into parts (unequal key ranges, costliest
+    first): the output matches the unsplit launch and, on sampled rows, the
+    float64 restatement of the int8 algorithm; repeated launches are
+    bit-identical."""
+    assert any(it[3] >= 0 for it in lk.pf_plan_items(m, P, near, 1, True)), "the plan splits"
+    K, V, Q = _inputs(oracle, m, P, 1.0, True)
+    note(f"pf auto split m={m} P={P} near={near}")
+    d = _Dev(lk, K, V, Q, m, P, False)
+    auto8 = d.attn8(lk, near, 1)
+    again8 = d.attn8(lk, near, 1)
+    try:
+        lk.pf_split_override(-1)
+        whole8 = d.attn8(lk, near, 1)
+    finally:
+        lk.pf_split_override(0)
+    assert np.array_equal(again8.view(np.uint32), auto8.view(np.uint32))
+    dw = oracle.rel_err(auto8, whole8)
+    rows = np.array(sorted({0, 1, 63, 64, 65, m // 2, m - 2, m - 1}), np.int32)
+    ref8 = oracle.pf_ref8(host(d.q8), host(d.qsc), host(d.qcs), Q, m, P, host(d.k8), host(d.ksc),
+                          d.kstride, K, V, near, 1, rows=rows)
+    r8 = oracle.rel_err(auto8, ref8)
+    note(f"  vs unsplit rel {dw:.3e}; rows {len(rows)} vs same-algorithm float64 rel {r8:.3e}")
+    assert dw <= 1e-3 and r8 <= 2e-3
+    assert np.isfinite(auto8).all()
+
+
 # ---- BASELINE prefill configurations (sampled rows against the float64 oracle) -----------------
 def _config_rows(m, long_ctx):
     rows = {0, 63, 64, 1023, m - 1} if long_ctx else \
