@@ -548,6 +548,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                     }
                 }
             } else {
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_setprio(1);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -589,17 +592,18 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                         }
                 }
             };
-            // The exponentials at raised wave priority.  The other wave on the
-            // SIMD is then mostly in its MFMA phases while this one runs the
-            // VALU-heavy softmax, and the two overlap more (with every phase at
-            // one priority the waves drift into the same phase: C5 72.6 ms
-            // against 67.9 ms with this, C4 127 against 121 us).
+            // Wave priorities by phase: exponent pass 2, int8 Q.K^T and the
+            // rest of the softmax 1, P.V 0.  The two waves of a SIMD (one per
+            // co-resident workgroup) then tend to be in different phases, VALU
+            // beside MFMA; at one priority for every phase they drift into the
+            // same phase (C5 72.6 ms against 66.0 ms with these levels; two
+            // adjacent phases at the same level lose the gain).
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_setprio(1);
+            __builtin_amdgcn_s_setprio(2);
             __builtin_amdgcn_sched_barrier(0);
             make_p();
             __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_s_setprio(1);
             __builtin_amdgcn_sched_barrier(0);
             unsigned pw[16];
 #pragma unroll
@@ -636,6 +640,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             }
         }
         // ---- O^T += V^T . P^T over the 64 keys, 32 per MFMA -----------------------
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
