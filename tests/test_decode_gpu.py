@@ -231,14 +231,15 @@ def test_config_c3_graph(lk, oracle):
     _check_config(lk, oracle, "C3", 10, [0, 9])
 
 
-def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle):
+@pytest.mark.parametrize("P0,steps", [(1000, 5), (0, 3), (14, 4), (2047, 3)])
+def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle, P0, steps):
     """The decode step graph (per layer: qk norm + RoPE + cache append folded
     into the split, combine; d_pos += 1 in the last combine) replayed n times =
     n decode steps: cache
     rows, d_pos and every layer's output against the oracle, and the replay
     bit-identical to the same kernels called eagerly."""
     rng = np.random.default_rng(61)
-    layers, P0, steps, cap = 3, 1000, 5, 1024
+    layers, cap = 3, 2048 + 64
     note(f"decode step graph: {layers} layers, {steps} steps from position {P0}")
     Ls, host_in = [], []
     for i in range(layers):
