@@ -455,7 +455,6 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         }
     }
 
-
 #ifdef PF_WG_TRACE
     const uint64_t t_q = __builtin_amdgcn_s_memrealtime();
 #endif
@@ -477,7 +476,8 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // as 2^(sq*(x - m) - PF_P_BIAS): a score at the headroom limit gives
     // p = 2^(8-7) = 2, the first fp16 value with bit 14 set, so "some p is past
     // the limit (or inf/NaN)" is one bit of the OR of all p.  p <= 2 keeps fp16
-    // far from overflow; p stays normal down to 2^-21 of the running max.  The
+    // far from overflow; p is a normal fp16 down to 2^-7 of the running max's
+    // p and below that keeps an absolute step of 2^-24 (2^-17 of it).  The
     // bias cancels in o = acc / l; partial records carry it in their max.
     constexpr float PF_HEADROOM = 8.0f;
     constexpr float PF_P_BIAS = 7.0f;
