@@ -80,6 +80,11 @@ def test_host_argument_errors():
     assert lib.lk_decode_graph_destroy(None) == 0
     assert lib.lk_decode_step_graph_create(0, None, p, p, p, ctypes.byref(h)) == 1
     assert lib.lk_decode_graph_run(None, 1, None) == 1
+    assert lib.lk_read_probe(None, 64, p, None) == 1
+    assert lib.lk_read_probe(p, 24, p, None) == 1                         # not a multiple of 16
+    assert lib.lk_pf_plan_items(0, 0, 0, 0, 1, None, 0) == -1
+    assert lib.lk_pf_plan_items(64, 0, 0, 0, 1, None, 4) == -1            # items NULL with room
+    assert lib.lk_pf_plan_items(64, 0, 0, 0, 1, None, 0) == 0             # one block: unsplit
 
 
 def test_python_mirror_fails_loudly_without_library(tmp_path):
