@@ -150,11 +150,18 @@ __host__ __device__ __forceinline__ void lk_attn_slices(int seq, int & ns, int &
 // (float) pos * f, each evaluated in fp64 and rounded once to fp32.
 #define LK_EPS_F        1e-5f
 #define LK_ROPE_THETA_D 10000000.0
-__device__ __forceinline__ void lk_rope_entry(int pos, int i, float & c, float & s) {
-    const float f = (float) pow(LK_ROPE_THETA_D, -(double) i / 32.0);
+__device__ __forceinline__ float lk_rope_freq(int i) {
+    return (float) pow(LK_ROPE_THETA_D, -(double) i / 32.0);
+}
+__device__ __forceinline__ void lk_rope_angle(int pos, float f, float & c, float & s) {
     const float a = (float) pos * f;                           // fp32 product, as the reference
-    c = (float) cos((double) a);
-    s = (float) sin((double) a);
+    double sd, cd;
+    sincos((double) a, &sd, &cd);
+    c = (float) cd;
+    s = (float) sd;
+}
+__device__ __forceinline__ void lk_rope_entry(int pos, int i, float & c, float & s) {
+    lk_rope_angle(pos, lk_rope_freq(i), c, s);
 }
 
 // ---- int8 row quantiser on 8-lane groups (shared by prefill.hip, qknr.hip) -----
