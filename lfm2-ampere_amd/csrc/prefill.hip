@@ -29,6 +29,7 @@
 #include "lk_common.h"
 #include <math.h>
 #include <algorithm>
+#include <type_traits>
 
 // ---------------------------------------------------------------------------
 // int8 quantisers.  Eight lanes per 64-wide (row, head), eight consecutive
@@ -735,11 +736,14 @@ lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work
     auto base = [&](int p) { return pbuf + (size_t) ((slot + p) * LK_N_KV_HEADS + kvh) * PF_PART_SLOT; };
     float M = -INFINITY, L = 0.0f;
     lk_f4 A[8] = {};
-    for (int p0 = 0; p0 < np; p0 += MAXP) {
-        float2 ml[MAXP];
-        lk_f4 a[MAXP][8];
+    // one pass over parts [p0, p0 + W): all loads first (one memory round
+    // trip), then the merge in part order
+    auto pass = [&](auto wc, int p0) {
+        constexpr int W = decltype(wc)::value;
+        float2 ml[W];
+        lk_f4 a[W][8];
 #pragma unroll
-        for (int i = 0; i < MAXP; ++i) {
+        for (int i = 0; i < W; ++i) {
             const int p = (p0 + i < np) ? p0 + i : p0;    // clamped: loads stay in bounds
             ml[i] = ((const float2 *) (base(p) + PF_PART_ACC))[h * PF_BQ + row];
             const lk_f4 * src = (const lk_f4 *) base(p) + (size_t) (h * 16 + 8 * hb) * PF_BQ + row;
@@ -748,13 +752,13 @@ lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work
         }
         float Mn = M;
 #pragma unroll
-        for (int i = 0; i < MAXP; ++i) if (p0 + i < np) Mn = fmaxf(Mn, ml[i].x);
+        for (int i = 0; i < W; ++i) if (p0 + i < np) Mn = fmaxf(Mn, ml[i].x);
         const float r = lk_exp2(M - Mn);                  // 0 on the first pass (M = -inf)
         L *= r;
 #pragma unroll
         for (int c = 0; c < 8; ++c) A[c] *= r;
 #pragma unroll
-        for (int i = 0; i < MAXP; ++i) {
+        for (int i = 0; i < W; ++i) {
             if (p0 + i >= np) break;
             const float wgt = lk_exp2(ml[i].x - Mn);
             L += ml[i].y * wgt;
@@ -762,7 +766,10 @@ lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work
             for (int c = 0; c < 8; ++c) A[c] += a[i][c] * wgt;
         }
         M = Mn;
-    }
+    };
+    // two parts per block is the common case: no redundant loads for it
+    if (np == 2) pass(std::integral_constant<int, 2>{}, 0);
+    else for (int p0 = 0; p0 < np; p0 += MAXP) pass(std::integral_constant<int, MAXP>{}, p0);
     const float il = 1.0f / L;
     float x[32];
 #pragma unroll
