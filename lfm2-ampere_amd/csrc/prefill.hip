@@ -942,6 +942,18 @@ static void pf_plan(int m, int P, int near, int sink, bool int8, PfWork & wk) {
         return (!int8 || lk_pf_exact(P, 2 * qt, kt, near, sink)) ? 1.4f : 1.0f;
     };
     constexpr float START = 2.1f;
+    // cost of key tiles [a, b) of block qt in closed form: the exact tiles of a
+    // block are tile 0 with the sink and the run from the first tile within
+    // `near` of the block's first 32 queries to the end (lk_pf_exact)
+    auto rcost = [&](int qt, int a, int b) -> float {
+        if (!int8) return START + 1.4f * (float) (b - a);
+        const int lim = P + 2 * qt * 32 - near;               // exact iff kt*64 + 64 > lim
+        const int kex = (lim < 64) ? 0 : (lim - 64) / 64 + 1;  // first such tile
+        int nex = b - ((a > kex) ? a : kex);
+        nex = (nex > 0) ? nex : 0;
+        if (sink && a == 0 && kex > 0 && b > 0) ++nex;           // tile 0, outside the run
+        return START + (float) (b - a) + 0.4f * (float) nex;
+    };
     constexpr int MAXP = 64;                           // pieces per block
     int cut[PF_MAX_QB][MAXP + 1];                      // piece boundaries per block
     int npc[PF_MAX_QB];
@@ -967,8 +979,7 @@ static void pf_plan(int m, int P, int near, int sink, bool int8, PfWork & wk) {
         float total = 0.0f, cmax = 0.0f;
         float bc[PF_MAX_QB];
         for (int qt = 0; qt < nq; ++qt) {
-            bc[qt] = START;
-            for (int kt = 0; kt < pf_nkt(qt, m, P); ++kt) bc[qt] += tcost(qt, kt);
+            bc[qt] = rcost(qt, 0, pf_nkt(qt, m, P));
             total += bc[qt];
             cmax = (bc[qt] > cmax) ? bc[qt] : cmax;
         }
@@ -1005,11 +1016,9 @@ static void pf_plan(int m, int P, int near, int sink, bool int8, PfWork & wk) {
         wk.slot0[qt] = (int16_t) (np > 1 ? slot : -1);
         wk.nparts[qt] = (uint8_t) np;
         if (np > 1) wk.split_qt[wk.n_split++] = (uint8_t) qt;
-        for (int p = 0; p < np; ++p) {
-            float c = START;
-            for (int kt = cut[qt][p]; kt < cut[qt][p + 1]; ++kt) c += tcost(qt, kt);
-            list[n++] = It{ c, qt, cut[qt][p], cut[qt][p + 1], np > 1 ? slot + p : -1 };
-        }
+        for (int p = 0; p < np; ++p)
+            list[n++] = It{ rcost(qt, cut[qt][p], cut[qt][p + 1]), qt, cut[qt][p], cut[qt][p + 1],
+                            np > 1 ? slot + p : -1 };
         if (np > 1) slot += np;
     }
     if (wk.n_split == 0) { wk.n_items = 0; return; }
