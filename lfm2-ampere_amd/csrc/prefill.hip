@@ -474,14 +474,22 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     const lk_h8 ones = { one, one, one, one, one, one, one, one };
     // The running max is only raised when a score exceeds it by more than
     // PF_HEADROOM (log2 units), so most tiles skip the rescale.  p is formed
-    // as 2^(sq*(x - m) - PF_P_BIAS): a score at the headroom limit gives
-    // p = 2^(8-7) = 2, the first fp16 value with bit 14 set, so "some p is past
-    // the limit (or inf/NaN)" is one bit of the OR of all p.  p <= 2 keeps fp16
-    // far from overflow; p is a normal fp16 down to 2^-7 of the running max's
-    // p and below that keeps an absolute step of 2^-24 (2^-17 of it).  The
-    // bias cancels in o = acc / l; partial records carry it in their max.
-    constexpr float PF_HEADROOM = 8.0f;
-    constexpr float PF_P_BIAS = 7.0f;
+    // as 2^(sq*(x - m) - PF_P_BIAS) with PF_HEADROOM = PF_P_BIAS + 1: a score
+    // at the headroom limit gives p = 2, the first fp16 value with bit 14 set,
+    // so "some p is past the limit (or inf/NaN)" is one bit of the OR of all p.
+    // p <= 2 keeps fp16 far from overflow.  With the bias 2^-5, p is a normal
+    // fp16 down to 2^-9 of the running max's p and below that keeps an
+    // absolute step of 2^-24 (2^-19 of it).  A larger bias trades accuracy on
+    // long diffuse rows for fewer rescales: at 2^-7 (headroom 8) rows over
+    // 8000 keys measured 8e-4 relative error against float64, at 2^-5 about
+    // 1e-4 to 2.6e-4 (as the unbiased form), with C5 unchanged and the 4096-key
+    // chunk 3% slower.  The bias cancels in o = acc / l; partial records carry
+    // it in their max.
+#ifndef PF_PBIAS
+#define PF_PBIAS 5
+#endif
+    constexpr float PF_P_BIAS = (float) PF_PBIAS;
+    constexpr float PF_HEADROOM = PF_P_BIAS + 1.0f;
 
     // ---- per-lane LDS read offsets: the swizzles above depend only on the lane
     // here, so every read below is one of these bases plus a constant.

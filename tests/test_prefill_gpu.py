@@ -227,7 +227,8 @@ def test_attn_split_parts(lk, oracle, m, P, near, L):
 
 
 # ---- the automatic (cost-model) split plan ------------------------------------------------------
-AUTO_CASES = [(1000, 0, 256), (777, 0, 1024), (1500, 300, 96), (2048, 777, 1024), (4096, 4096, 1024)]
+AUTO_CASES = [(1000, 0, 256), (777, 0, 1024), (1500, 300, 96), (2048, 777, 1024), (4096, 4096, 1024),
+              (512, 8000, 1024), (300, 20000, 256)]          # short chunks deep in a prompt: few blocks
 
 
 @pytest.mark.parametrize("m,P,near", AUTO_CASES, ids=[f"m{c[0]}_P{c[1]}_n{c[2]}" for c in AUTO_CASES])
