@@ -149,12 +149,14 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     // The barrier then covers the other waves' rows.
     auto wait_tile = [&](int it) {
         const int later = (ntile - 1 - it < D - 1) ? ntile - 1 - it : D - 1;
-        if (later >= 2)      lk_wait_vm<2 * RPW>();
+        if (later >= 4)      lk_wait_vm<4 * RPW>();
+        else if (later == 3) lk_wait_vm<3 * RPW>();
+        else if (later == 2) lk_wait_vm<2 * RPW>();
         else if (later == 1) lk_wait_vm<RPW>();
         else                 lk_wait_vm<0>();
         __builtin_amdgcn_s_barrier();
     };
-    static_assert(D - 1 <= 2, "wait_tile handles at most two later tiles in flight");
+    static_assert(D - 1 <= 4 && 4 * RPW <= 63, "wait_tile handles at most four later tiles in flight");
 
     // issue the first D tiles before anything else, so HBM starts streaming at once
 #pragma unroll

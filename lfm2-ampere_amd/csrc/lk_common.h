@@ -31,7 +31,7 @@
 #define LK_DEC_TILE        16
 #endif
 #ifndef LK_DEC_NBUF
-#define LK_DEC_NBUF        3
+#define LK_DEC_NBUF        4
 #endif
 
 // ---- vector types ---------------------------------------------------------------
