@@ -303,6 +303,27 @@ int lk_pf_plan_items(int m, int P, int near, int sink, int int8, int32_t * items
  * meets.  No counterpart in the reference. */
 int lk_read_probe(const void * src, size_t bytes, float * sink, void * stream);
 
+/* ---- the consumer of the decode attention output ------------------------ */
+
+/* Q4_0 x Q8_1 GEMV: replaces k_gemv_q4_0 (reference kernels.cu:300-306, body
+ * kernels.cu:190-260, block dot quant.cuh:131-158), launched for the attention
+ * output at engine.cu:655-657 with xq = the combine's yq8.
+ *   qs  : [out_rows][bpr] 16-byte Q4_0 quant blocks (byte j: element j in the
+ *         low nibble, element 16+j in the high nibble), 16-byte aligned
+ *   d   : [out_rows][bpr] fp16 block scales
+ *   xq  : [bpr] Q8_1 activation blocks (K = 32 * bpr, 1 <= bpr <= 256)
+ *   y   : [out_rows] fp32; y = (add_residual ? y : 0) + W.x (times the norm
+ *         scale below)
+ *   ssq : NULL, or the 64 sum-of-squares partials of an RMSNorm folded into the
+ *         activation's producer: the row result is multiplied by
+ *         1/sqrt((sum of ssq)/2048 + eps) (reference lk_norm_inv,
+ *         kernels.cuh:441-447)
+ * Per row the lane sums and the xor-butterfly follow the reference's warp
+ * (lane l takes blocks l, l+32, ...); fp32 steps round as written. */
+int lk_gemv_q4_0(const void * qs, const void * d, const lk_block_q8_1 * xq, int out_rows,
+                 int bpr, float * y, int add_residual, const float * ssq, float eps,
+                 void * stream);
+
 #ifdef __cplusplus
 }
 #endif

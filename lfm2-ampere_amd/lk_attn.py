@@ -32,7 +32,7 @@ EXPORTS = (
     "lk_pf_qk_i32", "lk_pf_plan_items", "lk_read_probe", "lk_qk_norm_rope", "lk_pf_qknr",
     "lk_decode_step_graph_create", "lk_decode_graph_run",
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
-    "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows",
+    "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows", "lk_gemv_q4_0",
 )
 
 
@@ -79,6 +79,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_qk_i32": ([P, I, P, I, P, P], I),
         "lk_pf_plan_items": ([I, I, I, I, I, P, I], I),
         "lk_read_probe": ([P, S, P, P], I),
+        "lk_gemv_q4_0": ([P, P, P, I, I, P, I, P, ctypes.c_float, P], I),
         "lk_qk_norm_rope": ([P, P, P, P, P, P, P, P, P], I),
         "lk_pf_qknr": ([P, P, P, I, I, P, P, P, P, P, I, P, P], I),
         "lk_decode_step_graph_create": ([I, P, P, P, P, P], I),
@@ -308,6 +309,17 @@ def read_probe(buf, sink, stream=None) -> None:
     """Plain streaming read of a device tensor (measurement reference)."""
     _check(load().lk_read_probe(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
                                 _stream(stream)), "lk_read_probe")
+
+
+def gemv_q4_0(qs, d, xq, out_rows: int, bpr: int, y, add_residual: bool = False, ssq=None,
+              eps: float = 1e-5, stream=None) -> None:
+    """Q4_0 x Q8_1 GEMV (reference k_gemv_q4_0): qs [out_rows][bpr] 16-byte
+    blocks, d fp16 [out_rows][bpr], xq [bpr] Q8_1 blocks (36 bytes), y fp32
+    [out_rows] (accumulated into when add_residual); ssq: 64 fp32 norm partials
+    or None."""
+    _check(load().lk_gemv_q4_0(_ptr(qs), _ptr(d), _ptr(xq), int(out_rows), int(bpr), _ptr(y),
+                               int(bool(add_residual)), _ptr(ssq), float(eps), _stream(stream)),
+           "lk_gemv_q4_0")
 
 
 def pf_plan_items(m: int, P: int, near: int, sink: int, int8: bool = True, max_items: int = 1024):

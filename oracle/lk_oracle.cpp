@@ -517,6 +517,72 @@ void lko_pf_qknr(const float * Y, const float * qn, const float * kn, int m, int
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_0 x Q8_1 block dot (reference quant.cuh:131-158): sumi = exact int sum of
+// nibble * q8 over the 32 elements (byte j of the 16-byte weight block holds
+// element j in its low nibble and element 16+j in its high nibble; nibbles are
+// 0..15, the -8 offset is carried by the activation sum); d4 = fp16 weight
+// scale; (d8, sum8) = the activation block's fp16 ds;
+// result = d4 * (d8 * (float) sumi - 8 * sum8), in fp32 as written.
+float lko_dot_q4_0_q8_1(const uint8_t * qs16, uint16_t d, const uint8_t * xq36) {
+    uint16_t dh, sh;
+    std::memcpy(&dh, xq36, 2);
+    std::memcpy(&sh, xq36 + 2, 2);
+    const int8_t * q8 = (const int8_t *) (xq36 + 4);
+    int sumi = 0;
+    for (int j = 0; j < 16; ++j) {
+        sumi += (int) (qs16[j] & 0x0F) * (int) q8[j];
+        sumi += (int) (qs16[j] >> 4) * (int) q8[16 + j];
+    }
+    const float d4 = lko_h2f(d), d8 = lko_h2f(dh), s8 = lko_h2f(sh);
+    const float t = d8 * (float) sumi;
+    const float u = 8.0f * s8;
+    return d4 * (t - u);
+}
+
+// Q4_0 GEMV (reference k_gemv_q4_0, kernels.cu:300-306, body kernels.cu:190-260
+// with LK_GEMV_ROWS = 1): row r is one 32-lane warp; lane l sums blocks
+// k = l, l+32, ... in order (fp32); warp_sum's xor-butterfly 16, 8, 4, 2, 1
+// (kernels.cuh:28-32) as lane 0 sees it; times ninv = 1/sqrt(s/2048 + eps)
+// when ssq is given, s = the same butterfly over ssq[l] + ssq[l+32]
+// (lk_norm_inv, kernels.cuh:441-447; evaluated in fp64 and rounded once, where
+// the reference uses the CUDA approximation rsqrtf); y[r] = add ? y[r] + a : a.
+static float lko_warp_sum32(const float * v) {
+    float s[32];
+    for (int i = 0; i < 32; ++i) s[i] = v[i];
+    for (int o = 16; o > 0; o >>= 1) {
+        float t[32];
+        for (int i = 0; i < 32; ++i) t[i] = s[i] + s[i ^ o];
+        std::memcpy(s, t, sizeof s);
+    }
+    return s[0];
+}
+
+void lko_gemv_q4_0(const uint8_t * qs, const uint16_t * d, const uint8_t * xq, int rows, int bpr,
+                   const float * ssq, float eps, float * y, int add) {
+    float ninv = 1.0f;
+    if (ssq) {
+        float v[32];
+        for (int l = 0; l < 32; ++l) v[l] = ssq[l] + ssq[l + 32];
+        const float s = lko_warp_sum32(v);
+        ninv = (float) (1.0 / std::sqrt((double) (s * (1.0f / 2048.0f) + eps)));
+    }
+    for (int r = 0; r < rows; ++r) {
+        float acc[32];
+        for (int l = 0; l < 32; ++l) {
+            float a = 0.0f;
+            for (int k = l; k < bpr; k += 32) {
+                const size_t b = (size_t) r * bpr + k;
+                a = a + lko_dot_q4_0_q8_1(qs + 16 * b, d[b], xq + 36 * (size_t) k);
+            }
+            acc[l] = a;
+        }
+        float a = lko_warp_sum32(acc);
+        if (ssq) a = a * ninv;
+        y[r] = add ? y[r] + a : a;
+    }
+}
+
 // max |a - b| / max |b| over n values (b is the reference).
 double lko_rel_err(const float * a, const double * b, size_t n) {
     double e = 0.0, r = 0.0;

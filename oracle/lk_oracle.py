@@ -59,6 +59,8 @@ def load():
         "lko_sm_student4": ([U64, P, S], None),
         "lko_mt_prefill_case": ([ctypes.c_uint32, I, I, F, I, P, P, P], None),
         "lko_rel_err": ([P, P, S], D),
+        "lko_dot_q4_0_q8_1": ([P, ctypes.c_uint16, P], F),
+        "lko_gemv_q4_0": ([P, P, P, I, I, P, F, P, I], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -275,6 +277,33 @@ def mt_prefill_case(seed: int, m: int, P: int, koff: float = 0.0, with_off: bool
     Q = np.empty(m * 2048, np.uint16)
     load().lko_mt_prefill_case(seed, m, P, koff, int(with_off), _p(K), _p(V), _p(Q))
     return K, V, Q
+
+
+def dot_q4_0_q8_1(qs16: np.ndarray, d: int, xq36: np.ndarray) -> float:
+    """One Q4_0 x Q8_1 block dot (reference quant.cuh:131-158), fp32."""
+    qs16 = np.ascontiguousarray(qs16, np.uint8)
+    xq36 = np.ascontiguousarray(xq36, np.uint8)
+    assert qs16.size == 16 and xq36.size == 36
+    return float(load().lko_dot_q4_0_q8_1(_p(qs16), int(d), _p(xq36)))
+
+
+def gemv_q4_0(qs, d, xq, rows, bpr, y=None, add=False, ssq=None, eps=1e-5) -> np.ndarray:
+    """Q4_0 GEMV (reference k_gemv_q4_0): qs uint8 [rows][bpr][16], d uint16
+    [rows][bpr], xq uint8 [bpr][36]; returns y float32 [rows]."""
+    qs = np.ascontiguousarray(qs, np.uint8)
+    d = np.ascontiguousarray(d, np.uint16)
+    xq = np.ascontiguousarray(xq, np.uint8)
+    assert qs.size == rows * bpr * 16 and d.size == rows * bpr and xq.size == bpr * 36
+    out = np.zeros(rows, np.float32) if y is None else np.array(y, np.float32).copy()
+    s = None if ssq is None else np.ascontiguousarray(ssq, np.float32)
+    load().lko_gemv_q4_0(_p(qs), _p(d), _p(xq), rows, bpr, _p(s), float(eps), _p(out), int(add))
+    return out
+
+
+def quantize_q8_1_blocks(x: np.ndarray) -> np.ndarray:
+    """fp32 [32 * n] -> Q8_1 blocks uint8 [n][36] (reference quant.cuh:106-121)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, 32)
+    return np.stack([quantize_q8_1(r) for r in x])
 
 
 def rel_err(a: np.ndarray, b: np.ndarray) -> float:

@@ -85,6 +85,15 @@ def test_host_argument_errors():
     assert lib.lk_pf_plan_items(0, 0, 0, 0, 1, None, 0) == -1
     assert lib.lk_pf_plan_items(64, 0, 0, 0, 1, None, 4) == -1            # items NULL with room
     assert lib.lk_pf_plan_items(64, 0, 0, 0, 1, None, 0) == 0             # one block: unsplit
+    F = ctypes.c_float
+    assert lib.lk_gemv_q4_0(None, p, p, 8, 64, p, 0, None, F(1e-5), None) == 1        # null qs
+    assert lib.lk_gemv_q4_0(p, p, p, 8, 0, p, 0, None, F(1e-5), None) == 1            # bpr < 1
+    assert lib.lk_gemv_q4_0(p, p, p, 8, 257, p, 0, None, F(1e-5), None) == 1          # bpr > 256
+    assert lib.lk_gemv_q4_0(p, p, p, -1, 64, p, 0, None, F(1e-5), None) == 1          # rows < 0
+    q = ctypes.c_void_p(0x1008)                                                        # not 16-byte aligned
+    assert lib.lk_gemv_q4_0(q, p, p, 8, 64, p, 0, None, F(1e-5), None) == 1
+    assert lib.lk_gemv_q4_0(p, p, p, 8, 64, p, 0, ctypes.c_void_p(0x1002), F(1e-5), None) == 1  # ssq
+    assert lib.lk_gemv_q4_0(None, None, None, 0, 64, None, 0, None, F(1e-5), None) == 0  # no rows
 
 
 def test_python_mirror_fails_loudly_without_library(tmp_path):

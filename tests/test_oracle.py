@@ -473,3 +473,79 @@ def test_pf_quant_rows_is_q8_1_widened(oracle):
             d = np.abs(x).max() / np.float32(127.0)
             if d > 0:
                 assert np.max(np.abs(qs[r, 32 * b:32 * b + 32] * d - x)) <= 0.5 * d * (1 + 1e-6)
+
+
+# ---- Q4_0 x Q8_1 dot and GEMV (the consumer of the decode attention output) -----------
+GOLDEN_Q4 = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "q4_0_dot.npz")
+
+
+def _golden_q4():
+    z = np.load(GOLDEN_Q4)
+    return [(z[f"qs{i}"], z[f"d{i}"], z[f"x{i}"], z[f"expected{i}"]) for i in range(int(z["n"]))]
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_dot_q4_0_reference_fixture(oracle, case):
+    """The reference's own golden vectors (ref/quant_fixture.bin: real attn_q
+    weight blocks, tests/test_quant.cu's gate): the block dots summed in order
+    against its expected_exact (ggml's integer convention in float64, with fp32
+    d8 and raw sums, hence the reference's 5e-3 bound) and expected_fp32."""
+    qs, d, x, (exact, fp32) = _golden_q4()[case]
+    xq = oracle.quantize_q8_1_blocks(x)
+    acc = np.float32(0.0)
+    for b in range(qs.shape[0]):
+        acc = np.float32(acc + np.float32(oracle.dot_q4_0_q8_1(qs[b], int(d[b]), xq[b])))
+    assert abs(acc - exact) / abs(exact) < 5e-3
+    assert abs(acc - fp32) / abs(fp32) < 5e-2
+    # and, tighter: the same formula in float64 on the fp16-rounded fields the
+    # Q8_1 block actually carries -- the oracle is then exact up to fp32 rounding
+    d4 = d.view(np.float16).astype(np.float64)
+    d8 = xq[:, 0:2].copy().view(np.float16).astype(np.float64).ravel()
+    s8 = xq[:, 2:4].copy().view(np.float16).astype(np.float64).ravel()
+    nib = np.concatenate([qs & 0x0F, qs >> 4], axis=1).astype(np.int64)
+    q8 = xq[:, 4:].view(np.int8).astype(np.int64)
+    want = float(np.sum(d4 * (d8 * (nib * q8).sum(1) - 8.0 * s8)))
+    assert abs(acc - want) <= 1e-5 * max(1.0, abs(want))
+
+
+def test_dot_q4_0_closed_form(oracle):
+    """Blocks whose Q8_1 fields are exact (d8 a power of two, sum representable):
+    then sum8 = d8 * sum(q8) and the block dot is the dequantised product
+    sum d4 * (nibble - 8) * d8 * q8 exactly.  Swapping the nibble halves, the
+    sign of the offset term or dropping a scale fails it."""
+    rng = np.random.default_rng(11)
+    for _ in range(200):
+        qs = rng.integers(0, 256, 16, dtype=np.uint8)
+        q8 = rng.integers(-20, 21, 32).astype(np.int8)
+        d8 = np.float16(2.0 ** int(rng.integers(-8, 0)))
+        s8 = np.float16(float(d8) * int(q8.astype(np.int64).sum()))
+        assert float(s8) == float(d8) * int(q8.astype(np.int64).sum())
+        xq = np.concatenate([np.array([d8, s8], np.float16).view(np.uint8), q8.view(np.uint8)])
+        d4 = np.float16(rng.uniform(0.001, 0.05))
+        w = np.concatenate([(qs & 0x0F).astype(np.int64) - 8, (qs >> 4).astype(np.int64) - 8])
+        want = float(d4) * float(d8) * float((w * q8.astype(np.int64)).sum())
+        got = oracle.dot_q4_0_q8_1(qs, int(np.array(d4).view(np.uint16)), xq)
+        assert abs(got - want) <= 2e-6 * max(1.0, abs(want)) + 1e-9
+
+
+def test_gemv_q4_0_rows_and_norm_scale(oracle):
+    """Each output row is the fp32 sum of its block dots (float64 within fp32
+    rounding), the residual is added, and the norm scale is
+    1/sqrt(sum(ssq)/2048 + eps)."""
+    rng = np.random.default_rng(5)
+    rows, bpr = 37, 70                       # bpr > 64: lanes take three blocks
+    qs = rng.integers(0, 256, (rows, bpr, 16), dtype=np.uint8)
+    d = rng.uniform(0.001, 0.02, (rows, bpr)).astype(np.float16).view(np.uint16)
+    xq = oracle.quantize_q8_1_blocks(rng.standard_normal(bpr * 32).astype(np.float32))
+    dots = np.array([[oracle.dot_q4_0_q8_1(qs[r, k], int(d[r, k]), xq[k]) for k in range(bpr)]
+                     for r in range(rows)], np.float64)
+    want = dots.sum(1)
+    y = oracle.gemv_q4_0(qs, d, xq, rows, bpr)
+    assert np.allclose(y, want, rtol=1e-5, atol=1e-6)
+    y0 = rng.standard_normal(rows).astype(np.float32)
+    ya = oracle.gemv_q4_0(qs, d, xq, rows, bpr, y=y0, add=True)
+    assert np.allclose(ya, y0.astype(np.float64) + want, rtol=1e-5, atol=1e-5)
+    ssq = rng.uniform(0.0, 50.0, 64).astype(np.float32)
+    yn = oracle.gemv_q4_0(qs, d, xq, rows, bpr, ssq=ssq, eps=1e-5)
+    ninv = 1.0 / math.sqrt(float(ssq.astype(np.float64).sum()) / 2048.0 + 1e-5)
+    assert np.allclose(yn, want * ninv, rtol=1e-5, atol=1e-6)
