@@ -111,11 +111,13 @@ def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters):
     return res
 
 
-def bench_decode_step(lk, steps, warmup, layers=10, ctx=32768):
+def bench_decode_step(lk, steps, warmup, layers=10, ctx=32768, with_wo=False):
     """The decode step graph (per layer: qk norm + RoPE + cache append, split,
     combine; then d_pos += 1; reference engine.cu:1328-1342,
     1750-1760) replayed `steps` times around a 32k context: the attention slice
-    of a whole decode step, producers included."""
+    of a whole decode step, producers included.  with_wo: each layer also runs
+    the attention output projection (x += W_o . yq8, 2048 x 2048 Q4_0,
+    engine.cu:655-657) as a third node."""
     import torch
     g = torch.Generator(device="cuda")
     g.manual_seed(91)
@@ -130,6 +132,11 @@ def bench_decode_step(lk, steps, warmup, layers=10, ctx=32768):
                    "kc": torch.randn(ctx, 8, 64, device="cuda", generator=g).half(),
                    "vc": torch.randn(ctx, 8, 64, device="cuda", generator=g).half(),
                    "out": torch.empty(32, 64, device="cuda")})
+        if with_wo:
+            Ls[-1].update({"out": None, "yq8": torch.zeros(64 * 36, dtype=torch.uint8, device="cuda"),
+                           "wo_qs": torch.randint(0, 256, (2048 * 64 * 16,), dtype=torch.uint8, device="cuda", generator=g),
+                           "wo_d": (torch.rand(2048 * 64, device="cuda", generator=g) * 0.02 + 0.001).half().view(torch.int16),
+                           "x": torch.zeros(2048, device="cuda")})
     start = ctx - steps - warmup
     d_pos = torch.tensor([start], dtype=torch.int32, device="cuda")
     part = torch.empty(lk.part_bytes() // 4, device="cuda")
@@ -275,6 +282,38 @@ def bench_read_reference(lk, bytes_list=(67108864, 268435456), nbuf=10, iters=20
         del bufs
         torch.cuda.empty_cache()
     return out
+
+
+def bench_gemv(lk, nmat=128, iters=256):
+    """The attention-output GEMV (reference k_gemv_q4_0 at engine.cu:655-657):
+    2048 x 2048 Q4_0 weights x the combine's 64 Q8_1 blocks, residual added.
+    Cycles over nmat distinct weight matrices (302 MB for 128, more than the
+    256 MB last-level cache), so every launch reads its weights from HBM as a
+    decode step does.  Algorithmic bytes per launch: 2048 x 64 x 18 (weights
+    and scales) + 64 x 36 (activation) + 2048 x 8 (residual read and write)."""
+    import torch
+    rows, bpr = 2048, 64
+    g = torch.Generator(device="cuda").manual_seed(7)
+    qs = [torch.randint(0, 256, (rows * bpr * 16,), dtype=torch.uint8, device="cuda", generator=g) for _ in range(nmat)]
+    d = [(torch.rand(rows * bpr, device="cuda", generator=g) * 0.02 + 0.001).half().view(torch.int16) for _ in range(nmat)]
+    xq = torch.zeros(bpr * 36, dtype=torch.uint8, device="cuda")
+    xq.view(bpr, 36)[:, 4:] = torch.randint(-127, 128, (bpr, 32), device="cuda", generator=g).to(torch.int8).view(torch.uint8)
+    xq.view(bpr, 36)[:, 0:2] = torch.full((bpr, 1), 0.01, device="cuda").half().view(torch.uint8)
+    y = torch.zeros(rows, device="cuda")
+    st = torch.cuda.Stream()
+    f = lambda i: lk.gemv_q4_0(qs[i % nmat], d[i % nmat], xq, rows, bpr, y, True, None, 1e-5, stream=st)
+    for i in range(nmat):
+        f(i)
+    st.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(iters):
+        f(i)
+    e1.record(st); e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    nbytes = rows * bpr * 18 + bpr * 36 + rows * 8
+    return {"rows": rows, "bpr": bpr, "us": us, "GBps": nbytes / (us * 1e-6) / 1e9, "bytes": nbytes,
+            "distinct_weight_matrices": nmat}
 
 
 def bench_producers(lk, iters):
@@ -481,6 +520,8 @@ def main():
     ap.add_argument("--profile-prefill", choices=["c4", "c5"], default=None,
                     help="only run --profile-launches int8 prefill attention launches (for rocprofv3 --pmc)")
     ap.add_argument("--profile-launches", type=int, default=3)
+    ap.add_argument("--profile-gemv", action="store_true",
+                    help="only run the attention-output GEMV bench (for rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this attention path is built and measured on a single "
@@ -499,6 +540,9 @@ def main():
     if args.profile_prefill:
         profile_prefill(lk, lkc, args.profile_prefill, args.profile_launches)
         return
+    if args.profile_gemv:
+        log(json.dumps(bench_gemv(lk)))
+        return
 
     log("decode C2 (32k x 10 layers, one hipGraph)")
     c2 = bench_decode(lk, lkc, "C2", args.steps, args.warmup, args.kernel_iters)
@@ -510,9 +554,15 @@ def main():
     log("practical HBM read rate (plain streaming read of the decode layer sizes)")
     results["hbm_read_reference"] = bench_read_reference(lk)
     log(json.dumps(results["hbm_read_reference"]))
+    log("attention-output GEMV (2048 x 2048 Q4_0 x Q8_1, residual add)")
+    results["attn_out_gemv"] = bench_gemv(lk)
+    log(json.dumps(results["attn_out_gemv"]))
     log("decode step graph (producer + attention, 10 layers, 32k context)")
     results["C2_decode_step_graph"] = bench_decode_step(lk, 50, 10)
     log(json.dumps(results["C2_decode_step_graph"]))
+    log("decode step graph with the attention output projection (3 nodes per layer)")
+    results["C2_decode_step_graph_wo"] = bench_decode_step(lk, 50, 10, with_wo=True)
+    log(json.dumps(results["C2_decode_step_graph_wo"]))
     if not args.skip_prefill:
         log("prefill C4 (4096 chunk, P=0)")
         results["C4_prefill_4k"] = bench_prefill_c4(lk, lkc, 20)

@@ -125,8 +125,8 @@ int lk_decode_graph_destroy(lk_decode_graph * graph);
  * layer's cache (lk_qk_norm_rope's arithmetic, out of place), split and
  * combine; then *d_pos += 1.  The producer runs inside the split kernel (each
  * workgroup forms q itself; the one whose slice holds *d_pos appends K/V and
- * uses the new row directly), so a layer is two graph nodes; the last
- * layer's combine advances *d_pos.
+ * uses the new row directly), so a layer is two graph nodes (three with the
+ * optional output projection below); the last layer's combine advances *d_pos.
  * Replaying it n times runs n decode steps with no host work in between.
  * All pointers are device pointers owned by the caller; `part` is shared by
  * the layers. */
@@ -142,6 +142,12 @@ typedef struct lk_decode_layer {
     void *        vc;               /* fp16 [max_seq][8][64] */
     float *       out;              /* fp32 [32][64] or NULL */
     lk_block_q8_1 * yq8;            /* [64] or NULL */
+    /* Optional third node, the attention output projection (reference
+     * engine.cu:655-657): when wo_qs is not NULL, x += W_o . yq8 by
+     * lk_gemv_q4_0 after the combine (yq8 and x required). */
+    const void *  wo_qs;            /* Q4_0 [2048][64] 16-byte blocks, or NULL */
+    const void *  wo_d;             /* fp16 [2048][64] block scales */
+    float *       x;                /* fp32 [2048] residual stream */
 } lk_decode_layer;
 int lk_decode_step_graph_create(int n_layers, const lk_decode_layer * layers, int * d_pos,
                                 float * part, void * stream, lk_decode_graph ** graph);

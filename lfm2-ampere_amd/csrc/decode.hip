@@ -625,6 +625,8 @@ extern "C" int lk_decode_step_graph_create(int n_layers, const lk_decode_layer *
         const lk_decode_layer & L = layers[i];
         if (!L.q_src || !L.k_src || !L.v_src || !L.q || !L.k || !L.q_norm || !L.k_norm || !L.kc || !L.vc)
             return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: null pointer for layer %d", i);
+        if (L.wo_qs && (!L.wo_d || !L.x || !L.yq8))
+            return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: layer %d: the output projection needs wo_d, x and yq8", i);
     }
     hipStream_t st = lk_stream(stream);
     hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
@@ -637,6 +639,9 @@ extern "C" int lk_decode_step_graph_create(int n_layers, const lk_decode_layer *
         rc = lk_split_fused_launch(L, d_pos, part, st);
         // the last layer's combine also advances *d_pos
         if (!rc) rc = lk_combine_launch(part, d_pos, L.out, L.yq8, st, i == n_layers - 1 ? d_pos : nullptr);
+        // optional: the attention output projection into the residual stream
+        if (!rc && L.wo_qs)
+            rc = lk_gemv_q4_0(L.wo_qs, L.wo_d, L.yq8, LK_HIDDEN, LK_HIDDEN / 32, L.x, 1, nullptr, 0.0f, st);
     }
     hipGraph_t g = nullptr;
     e = hipStreamEndCapture(st, &g);

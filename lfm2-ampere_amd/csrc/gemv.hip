@@ -28,9 +28,9 @@
 // MI355X design: one row per 32-lane half of a wave (the reference's warp, so
 // the lane -> block mapping and the butterfly are the reference's), 8 rows per
 // 256-thread workgroup, 256 workgroups for 2048 rows.  Each lane issues all of
-// its loads at once -- 16-byte weight blocks, their fp16 scales and the 36-byte
+// its loads at once -- 16-byte weight blocks, their fp16 scales, the 36-byte
 // activation blocks (as nine dwords; 2.3 KB in total, read by every row from
-// L2) -- and forms sumi with v_dot4_i32_i8 (nibbles 0..15 are non-negative
+// L2) and the residual -- and forms sumi with v_dot4_i32_i8 (nibbles 0..15 are non-negative
 // int8 values, so the signed dot is exact).  HBM-bound on the weights: 18
 // bytes per 32 weights, 2.36 MB for the 2048 x 2048 attention output matrix.
 #include "lk_common.h"
@@ -83,6 +83,7 @@ lk_k_gemv_q4_0(const uint4 * __restrict__ qs, const _Float16 * __restrict__ d,
     }
     float ss = 0.0f;
     if (ssq) ss = ssq[l] + ssq[l + 32];
+    const float yr = add_residual ? y[rowc] : 0.0f;      // issued with the other loads
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < NK; ++i)
@@ -95,7 +96,7 @@ lk_k_gemv_q4_0(const uint4 * __restrict__ qs, const _Float16 * __restrict__ d,
         const float ninv = (float) (1.0 / sqrt((double) (ss * (1.0f / (float) LK_HIDDEN) + eps)));
         acc = acc * ninv;
     }
-    if (live && l == 0) y[row] = add_residual ? y[row] + acc : acc;
+    if (live && l == 0) y[row] = add_residual ? yr + acc : acc;
 }
 
 template <int NK>

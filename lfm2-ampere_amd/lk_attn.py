@@ -167,7 +167,8 @@ def attention_decode(q, kc, vc, d_pos, out=None, yq8=None, stream=None) -> None:
 class DecodeLayer(ctypes.Structure):
     """lk_decode_layer (include/lk_attn.h): one layer's buffers for the step graph."""
     _fields_ = [(n, ctypes.c_void_p) for n in
-                ("q_src", "k_src", "v_src", "q", "k", "q_norm", "k_norm", "kc", "vc", "out", "yq8")]
+                ("q_src", "k_src", "v_src", "q", "k", "q_norm", "k_norm", "kc", "vc", "out", "yq8",
+                 "wo_qs", "wo_d", "x")]
 
 
 class DecodeStepGraph:

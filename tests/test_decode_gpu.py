@@ -302,6 +302,48 @@ def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle, P0, steps):
     g.close()
 
 
+def test_decode_step_graph_with_output_projection(lk, oracle):
+    """The step graph with the optional third node per layer (x += W_o . yq8,
+    lk_gemv_q4_0): three nodes per layer, and after each replay every layer's
+    residual stream equals the oracle's GEMV of that step's Q8_1 blocks added
+    to the previous x, bit for bit."""
+    rng = np.random.default_rng(62)
+    layers, cap, P0, steps = 2, 1024, 500, 3
+    note(f"decode step graph with the output projection: {layers} layers, {steps} steps")
+    Ls, W = [], []
+    for i in range(layers):
+        wq = rng.integers(0, 256, (2048, 64, 16), dtype=np.uint8)
+        wd = rng.uniform(0.002, 0.02, (2048, 64)).astype(np.float16).view(np.uint16)
+        W.append((wq, wd))
+        kc0 = np.zeros((cap, 8, 64), np.uint16)
+        vc0 = np.zeros((cap, 8, 64), np.uint16)
+        kc0[:P0] = rng.standard_normal((P0, 8, 64)).astype(np.float16).view(np.uint16)
+        vc0[:P0] = rng.standard_normal((P0, 8, 64)).astype(np.float16).view(np.uint16)
+        Ls.append({"q_src": dev((rng.standard_normal(2048) * 2).astype(np.float32)),
+                   "k_src": dev((rng.standard_normal(512) * 2).astype(np.float32)),
+                   "v_src": dev(rng.standard_normal(512).astype(np.float32)),
+                   "q": torch.empty(2048, device="cuda"), "k": torch.empty(512, device="cuda"),
+                   "q_norm": dev(rng.uniform(0.5, 1.5, 64).astype(np.float32)),
+                   "k_norm": dev(rng.uniform(0.5, 1.5, 64).astype(np.float32)),
+                   "kc": dev_h(kc0), "vc": dev_h(vc0), "out": None,
+                   "yq8": torch.zeros(64 * 36, dtype=torch.uint8, device="cuda"),
+                   "wo_qs": dev(wq.reshape(-1)), "wo_d": dev(wd.reshape(-1).view(np.int16)),
+                   "x": dev(rng.standard_normal(2048).astype(np.float32))})
+    d_pos = torch.tensor([P0], dtype=torch.int32, device="cuda")
+    part = torch.empty(lk.part_bytes() // 4, device="cuda")
+    g = lk.DecodeStepGraph(Ls, d_pos, part)
+    assert g.nodes() == 3 * layers
+    for s in range(steps):
+        x_before = [host(L["x"]).copy() for L in Ls]
+        g.run(1)
+        g.stream.synchronize()
+        for (wq, wd), L, x0 in zip(W, Ls, x_before):
+            want = oracle.gemv_q4_0(wq, wd, host(L["yq8"]).reshape(64, 36), 2048, 64, y=x0, add=True)
+            assert np.array_equal(host(L["x"]).view(np.uint32), want.view(np.uint32)), s
+    assert int(d_pos.item()) == P0 + steps
+    g.close()
+
+
 def test_read_probe_reads_and_leaves_sink(lk):
     """The measurement probe (not on the attention path) runs over a buffer and
     leaves its sink untouched; misaligned sizes are rejected."""
