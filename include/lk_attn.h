@@ -330,6 +330,23 @@ int lk_gemv_q4_0(const void * qs, const void * d, const lk_block_q8_1 * xq, int 
                  int bpr, float * y, int add_residual, const float * ssq, float eps,
                  void * stream);
 
+/* Q4_0 x planar Q8_1 GEMM for a prefill chunk: replaces pf_gemm_dense with one
+ * weight tensor and the plain epilogue (reference k_pf_mmq EPI 0,
+ * prefill.cu:173-490 with PF_EPI2; pf_gemm_dense prefill.cu:818-826; PfGemm,
+ * prefill.cuh:38-69), launched for the attention output at engine.cu:1128-1131
+ * with (aqs, asc) = the planar Q8_1 lk_pf_attn8_q81 writes.
+ *   qs  : [N][bpr] 16-byte Q4_0 blocks (16-byte aligned), d: [N][bpr] fp16
+ *   aqs : int8 [ntok][bpr * 32]; asc: float2 [ntok][bpr] = (d8, 8 * sum)
+ *   out : fp32 [ntok][out_ld] (16-byte aligned, out_ld a multiple of 4, >= N);
+ *         out[t][r] = (add ? out[t][r] : 0) + scale[t] * sum over blocks
+ *   scale: fp32 [ntok] or NULL (1)
+ * N must be a multiple of 64.  Per (t, r) the blocks are accumulated in order
+ * with the reference's fma sequence; the epilogue rounds the product and the
+ * sum separately, as the reference's source writes them. */
+int lk_pf_gemm_q4_0(const void * qs, const void * d, int N, int bpr, const int8_t * aqs,
+                    const float * asc, int ntok, const float * scale, float * out, int out_ld,
+                    int add, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

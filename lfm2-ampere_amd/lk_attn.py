@@ -32,7 +32,7 @@ EXPORTS = (
     "lk_pf_qk_i32", "lk_pf_plan_items", "lk_read_probe", "lk_qk_norm_rope", "lk_pf_qknr",
     "lk_decode_step_graph_create", "lk_decode_graph_run",
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
-    "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows", "lk_gemv_q4_0",
+    "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows", "lk_gemv_q4_0", "lk_pf_gemm_q4_0",
 )
 
 
@@ -80,6 +80,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_plan_items": ([I, I, I, I, I, P, I], I),
         "lk_read_probe": ([P, S, P, P], I),
         "lk_gemv_q4_0": ([P, P, P, I, I, P, I, P, ctypes.c_float, P], I),
+        "lk_pf_gemm_q4_0": ([P, P, I, I, P, P, I, P, P, I, I, P], I),
         "lk_qk_norm_rope": ([P, P, P, P, P, P, P, P, P], I),
         "lk_pf_qknr": ([P, P, P, I, I, P, P, P, P, P, I, P, P], I),
         "lk_decode_step_graph_create": ([I, P, P, P, P, P], I),
@@ -321,6 +322,15 @@ def gemv_q4_0(qs, d, xq, out_rows: int, bpr: int, y, add_residual: bool = False,
     _check(load().lk_gemv_q4_0(_ptr(qs), _ptr(d), _ptr(xq), int(out_rows), int(bpr), _ptr(y),
                                int(bool(add_residual)), _ptr(ssq), float(eps), _stream(stream)),
            "lk_gemv_q4_0")
+
+
+def pf_gemm_q4_0(qs, d, N: int, bpr: int, aqs, asc, ntok: int, out, out_ld: int = None,
+                 add: bool = False, scale=None, stream=None) -> None:
+    """Q4_0 x planar Q8_1 GEMM of a prefill chunk (reference pf_gemm_dense, one
+    tensor, plain epilogue): out[t][r] (+)= scale[t] * W[r] . x[t]."""
+    _check(load().lk_pf_gemm_q4_0(_ptr(qs), _ptr(d), int(N), int(bpr), _ptr(aqs), _ptr(asc), int(ntok),
+                                  _ptr(scale), _ptr(out), int(N if out_ld is None else out_ld),
+                                  int(bool(add)), _stream(stream)), "lk_pf_gemm_q4_0")
 
 
 def pf_plan_items(m: int, P: int, near: int, sink: int, int8: bool = True, max_items: int = 1024):

@@ -583,6 +583,36 @@ void lko_gemv_q4_0(const uint8_t * qs, const uint16_t * d, const uint8_t * xq, i
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_0 x planar Q8_1 GEMM, dense, plain epilogue (reference k_pf_mmq EPI 0 with
+// PF_EPI2, prefill.cu:131-141, 330-390, 470-490; pf_gemm_dense prefill.cu:818-826):
+// for token t and row r, over the blocks b in order: F = 1.5*2^23 + sumi
+// (exact), c = fma(d8, 1.5*2^23, s8), acc = fma(d4, fma(d8, F, -c), acc), with
+// (d8, s8) = asc[t][b] (s8 = 8 * fp16 sum) and d4 = d[r][b]; then
+// a = acc * scale[t] (1 without scale) and out[t][r] = add ? out[t][r] + a : a.
+// qs [N][bpr][16], d fp16 [N][bpr], aqs int8 [ntok][bpr * 32], asc [ntok][bpr][2].
+void lko_pf_gemm_q4_0(const uint8_t * qs, const uint16_t * d, int N, int bpr, const int8_t * aqs,
+                      const float * asc, int ntok, const float * scale, float * out, int out_ld, int add) {
+    const float M = 12582912.0f;
+    for (int t = 0; t < ntok; ++t)
+        for (int r = 0; r < N; ++r) {
+            float acc = 0.0f;
+            for (int b = 0; b < bpr; ++b) {
+                const uint8_t * q = qs + ((size_t) r * bpr + b) * 16;
+                const int8_t * x = aqs + (size_t) t * bpr * 32 + (size_t) b * 32;
+                int sumi = 0;
+                for (int j = 0; j < 16; ++j) sumi += (int) (q[j] & 0x0F) * x[j] + (int) (q[j] >> 4) * x[16 + j];
+                const float F = M + (float) sumi;                 // exact: |sumi| < 2^22
+                const float d8 = asc[((size_t) t * bpr + b) * 2], s8 = asc[((size_t) t * bpr + b) * 2 + 1];
+                const float c = std::fmaf(d8, M, s8);
+                acc = std::fmaf(lko_h2f(d[(size_t) r * bpr + b]), std::fmaf(d8, F, -c), acc);
+            }
+            const float a = acc * (scale ? scale[t] : 1.0f);
+            float & o = out[(size_t) t * out_ld + r];
+            o = add ? o + a : a;
+        }
+}
+
 // max |a - b| / max |b| over n values (b is the reference).
 double lko_rel_err(const float * a, const double * b, size_t n) {
     double e = 0.0, r = 0.0;

@@ -61,6 +61,7 @@ def load():
         "lko_rel_err": ([P, P, S], D),
         "lko_dot_q4_0_q8_1": ([P, ctypes.c_uint16, P], F),
         "lko_gemv_q4_0": ([P, P, P, I, I, P, F, P, I], None),
+        "lko_pf_gemm_q4_0": ([P, P, I, I, P, P, I, P, P, I, I], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -298,6 +299,20 @@ def gemv_q4_0(qs, d, xq, rows, bpr, y=None, add=False, ssq=None, eps=1e-5) -> np
     s = None if ssq is None else np.ascontiguousarray(ssq, np.float32)
     load().lko_gemv_q4_0(_p(qs), _p(d), _p(xq), rows, bpr, _p(s), float(eps), _p(out), int(add))
     return out
+
+
+def pf_gemm_q4_0(qs, d, N, bpr, aqs, asc, ntok, scale=None, out=None, out_ld=None, add=False) -> np.ndarray:
+    """Q4_0 x planar Q8_1 GEMM (reference k_pf_mmq EPI 0): qs uint8 [N][bpr][16],
+    d uint16 [N][bpr], aqs int8 [ntok][bpr*32], asc float32 [ntok][bpr][2];
+    returns out float32 [ntok][out_ld]."""
+    out_ld = N if out_ld is None else out_ld
+    qs = np.ascontiguousarray(qs, np.uint8); d = np.ascontiguousarray(d, np.uint16)
+    aqs = np.ascontiguousarray(aqs, np.int8); asc = np.ascontiguousarray(asc, np.float32)
+    assert qs.size == N * bpr * 16 and d.size == N * bpr and aqs.size >= ntok * bpr * 32 and asc.size >= ntok * bpr * 2
+    o = np.zeros((ntok, out_ld), np.float32) if out is None else np.array(out, np.float32).reshape(ntok, out_ld).copy()
+    sc = None if scale is None else np.ascontiguousarray(scale, np.float32)
+    load().lko_pf_gemm_q4_0(_p(qs), _p(d), N, bpr, _p(aqs), _p(asc), ntok, _p(sc), _p(o), out_ld, int(add))
+    return o
 
 
 def quantize_q8_1_blocks(x: np.ndarray) -> np.ndarray:

@@ -549,3 +549,47 @@ def test_gemv_q4_0_rows_and_norm_scale(oracle):
     yn = oracle.gemv_q4_0(qs, d, xq, rows, bpr, ssq=ssq, eps=1e-5)
     ninv = 1.0 / math.sqrt(float(ssq.astype(np.float64).sum()) / 2048.0 + 1e-5)
     assert np.allclose(yn, want * ninv, rtol=1e-5, atol=1e-6)
+
+
+def test_pf_gemm_q4_0_reference_fixture(oracle):
+    """The prefill GEMM restatement on the reference's golden Q4_0 blocks: one
+    token, the input quantised to planar Q8_1 (lko_pf_quant_rows), against
+    expected_exact / expected_fp32 with the reference's gate bounds."""
+    for qs, d, x, (exact, fp32) in _golden_q4():
+        bpr = qs.shape[0]
+        aqs, asc = oracle.pf_quant_rows(x.reshape(1, -1), 1, bpr * 32, bpr)
+        # the same row 64 times (N is a multiple of 64 in the GEMM's interface)
+        got = float(oracle.pf_gemm_q4_0(np.tile(qs[None], (64, 1, 1)), np.tile(d[None], (64, 1)),
+                                        64, bpr, aqs, asc, 1)[0, 0])
+        assert abs(got - exact) / abs(exact) < 5e-3
+        assert abs(got - fp32) / abs(fp32) < 5e-2
+
+
+def test_pf_gemm_q4_0_block_formula(oracle):
+    """Against float64 sum_b d4 * (d8 * sumi - s8): the only rounding the
+    restatement adds beyond fp32 accumulation is the magic constant's (half a
+    unit of sumi per block); a swapped nibble half, a transposed operand or a
+    dropped offset term is off by far more.  Residual add and per-token scale."""
+    rng = np.random.default_rng(9)
+    N, bpr, ntok = 64, 5, 7
+    qs = rng.integers(0, 256, (N, bpr, 16), dtype=np.uint8)
+    d = rng.uniform(0.002, 0.02, (N, bpr)).astype(np.float16).view(np.uint16)
+    aqs, asc = oracle.pf_quant_rows(rng.standard_normal((ntok, bpr * 32)).astype(np.float32), ntok, bpr * 32, bpr)
+    nib = np.concatenate([qs & 0x0F, qs >> 4], axis=2).astype(np.int64)                 # [N][bpr][32]
+    xq = aqs.reshape(ntok, bpr, 32).astype(np.int64)
+    sumi = np.einsum("rbk,tbk->trb", nib, xq).astype(np.float64)
+    sc = asc.reshape(ntok, bpr, 2).astype(np.float64)
+    d4 = d.view(np.float16).astype(np.float64)
+    want = np.einsum("rb,trb->tr", d4, sc[:, None, :, 0] * sumi - sc[:, None, :, 1])
+    got = oracle.pf_gemm_q4_0(qs, d, N, bpr, aqs, asc, ntok)
+    # the constant c = fma(d8, 1.5*2^23, s8) rounds once per block (at most one
+    # ulp of c, about one unit of sumi); fp32 accumulation adds ~1e-6 relative
+    c = (sc[:, :, 0] * 12582912.0 + sc[:, :, 1]).astype(np.float32)                  # [ntok][bpr]
+    bound = np.einsum("rb,tb->tr", np.abs(d4), np.spacing(np.abs(c)).astype(np.float64)) \
+        + 1e-6 * np.einsum("rb,trb->tr", np.abs(d4), np.abs(sc[:, None, :, 0] * sumi - sc[:, None, :, 1]))
+    assert np.all(np.abs(got - want) <= bound)
+    assert np.max(bound) < 1e-3 * np.max(np.abs(want))          # the bound itself is tight
+    y0 = rng.standard_normal((ntok, N)).astype(np.float32)
+    s = rng.uniform(0.5, 2.0, ntok).astype(np.float32)
+    got2 = oracle.pf_gemm_q4_0(qs, d, N, bpr, aqs, asc, ntok, scale=s, out=y0, add=True)
+    assert np.allclose(got2, y0 + got * s[:, None], rtol=1e-6, atol=1e-6)
