@@ -316,6 +316,28 @@ def bench_gemv(lk, nmat=128, iters=256):
             "distinct_weight_matrices": nmat}
 
 
+def bench_pf_gemm(lk, ntok=4096, N=2048, bpr=64, iters=20):
+    """The attention-output GEMM of a prefill chunk (reference pf_gemm_dense at
+    engine.cu:1128-1131): C4's 4096 tokens of planar Q8_1 x 2048 x 2048 Q4_0,
+    residual added.  Work: 2 * N * 32 * bpr * ntok int8 ops (the nibble x int8
+    products and sums)."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(11)
+    qs = torch.randint(0, 256, (N * bpr * 16,), dtype=torch.uint8, device="cuda", generator=g)
+    d = (torch.rand(N * bpr, device="cuda", generator=g) * 0.02 + 0.001).half().view(torch.int16)
+    aqs = torch.randint(-127, 128, (ntok, bpr * 32), device="cuda", generator=g).to(torch.int8)
+    asc = torch.rand(ntok, bpr, 2, device="cuda", generator=g) * 0.02
+    out = torch.zeros(ntok, N, device="cuda")
+    st = torch.cuda.Stream()
+    f = lambda: lk.pf_gemm_q4_0(qs, d, N, bpr, aqs, asc, ntok, out, N, True, stream=st)
+    for _ in range(iters):
+        f()
+    ms = timed_events(f, st, iters)
+    ops = 2.0 * N * 32 * bpr * ntok
+    return {"ntok": ntok, "N": N, "K": 32 * bpr, "us": ms * 1e3, "TOPS": ops / (ms * 1e-3) / 1e12,
+            "frac_of_int8_peak": ops / (ms * 1e-3) / (PEAK_INT8_TOPS * 1e12)}
+
+
 def bench_producers(lk, iters):
     """The attention-input producers (reference kernels.cu:871-915,
     prefill.cu:975-1016): the prefill pass over one 4096-token chunk (C4's
@@ -542,6 +564,7 @@ def main():
         return
     if args.profile_gemv:
         log(json.dumps(bench_gemv(lk)))
+        log(json.dumps(bench_pf_gemm(lk)))
         return
 
     log("decode C2 (32k x 10 layers, one hipGraph)")
@@ -570,6 +593,9 @@ def main():
         log("prefill C5 (131072 prompt, 32 chunks)")
         results["C5_prefill_131k"] = bench_prefill_c5(lk, lkc, 2)
         log(json.dumps(results["C5_prefill_131k"]))
+        log("prefill attention-output GEMM (4096 tokens x 2048 x 2048 Q4_0)")
+        results["pf_attn_out_gemm"] = bench_pf_gemm(lk)
+        log(json.dumps(results["pf_attn_out_gemm"]))
         log("attention-input producers (qk norm + rope + cache write)")
         results["producers"] = bench_producers(lk, 20)
         log(json.dumps(results["producers"]))

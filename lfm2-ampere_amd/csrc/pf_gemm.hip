@@ -25,20 +25,37 @@
 // operand: lane l supplies weight row l%16, elements 8(l/16)..+7, i.e. the low
 // or high nibbles of bytes 0-7 or 8-15 of the 16-byte block (one shift, one
 // mask); B operand: 8 int8 of the activation row.  The accumulator is seeded
-// with 0x4B400000 so the integer sum arrives as the float F.  The fp16 weight
-// scales and the (d8, 8 sum) token scales of 32 blocks at a time are staged in
-// LDS ([block][row] and [block][token]), so a lane reads its 4 rows' d4 as one
-// 8-byte read; operands come straight from L2 into registers, 4 blocks ahead.
-// The output tile is written as float4 (4 consecutive rows of one token).
+// with 0x4B400000 so the integer sum arrives as the float F.  Staging: 8 blocks
+// at a time of the weight quants, the activation quants, the fp16 weight
+// scales and the (d8, 8 sum) token scales go through LDS in two stages (each
+// thread one 16-byte-coalesced quarter-row of each plane; the next stage's
+// global loads are in flight while the current one is computed); rows are
+// padded by 16 bytes, the scales kept as [block][row] and [block][token], so a
+// lane reads its 4 rows' d4 as one 8-byte read.  Loading the operands straight
+// from L2 instead (8 scattered bytes per lane) measured 240 us against 95 us
+// for C4's 4096 x 2048 x 2048.  The output tile is written as float4 (4
+// consecutive rows of one token).  Needs bpr % 8 == 0, as the reference's
+// pf_gemm_dense does.
 #include "lk_common.h"
 
 #define PFG_BM 64                  // weight rows per workgroup
 #define PFG_BN 64                  // tokens per workgroup
-#define PFG_KC 32                  // blocks staged in LDS at a time
-#define PFG_AHEAD 4                // blocks of operands in flight
+#define PFG_KC 8                   // blocks per LDS stage (the staging below moves exactly 8)
+#define PFG_AP (PFG_KC * 16 + 16)  // LDS pitch of a weight row (bytes, padded)
+#define PFG_BP (PFG_KC * 32 + 16)  // LDS pitch of an activation row
+#ifndef PFG_ABL
+#define PFG_ABL 0                  // measurement builds only: 2 no MFMA, 4 no fma epilogue
+#endif
 
 typedef int lk_i4g __attribute__((ext_vector_type(4)));
 typedef float lk_f4g __attribute__((ext_vector_type(4)));
+
+struct alignas(16) PfgStage {
+    uint8_t  a[PFG_BM * PFG_AP];     // weight quant blocks [row][block][16]
+    int8_t   b[PFG_BN * PFG_BP];     // activation quants [token][block][32]
+    _Float16 d[PFG_KC][PFG_BM];      // weight scales [block][row]
+    float2   s[PFG_KC][PFG_BN];      // token scales (d8, 8 sum) [block][token]
+};
 
 template <bool ADD>
 __global__ void __launch_bounds__(256, 2)
@@ -46,8 +63,7 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
                   const int8_t * __restrict__ aqs, const float2 * __restrict__ asc, int ntok,
                   const float * __restrict__ scale, float * __restrict__ out, int out_ld) {
 #pragma clang fp contract(off)
-    __shared__ __attribute__((aligned(16))) _Float16 s_d[PFG_KC][PFG_BM];   // [block][row]
-    __shared__ __attribute__((aligned(16))) float2 s_s[PFG_KC][PFG_BN];     // [block][token]
+    __shared__ PfgStage stg[2];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = blockIdx.x * PFG_BM, tok0 = blockIdx.y * PFG_BN;
@@ -55,86 +71,101 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
     const int l16 = lane & 15, kg = lane >> 4;
     constexpr float MAGIC = 12582912.0f;               // 1.5 * 2^23 = float bits 0x4B400000
 
-    // per-lane operand sources (row / token clamped: loads stay in bounds)
-    const uint8_t * ap[2];
-    const int8_t * bp[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        ap[i] = qs + ((size_t) (row0 + wr + 16 * i + l16) * bpr) * 16 + 8 * (kg & 1);
-        const int t = tok0 + wt + 16 * i + l16;
-        bp[i] = aqs + (size_t) (t < ntok ? t : ntok - 1) * bpr * 32 + 8 * kg;
-    }
-    const int sh = 4 * (kg >> 1);                      // low or high nibbles
+    // ---- staging: thread t moves row / token t/4, quarter t%4 of each plane --
+    static_assert(PFG_KC == 8 && PFG_BM == 64 && PFG_BN == 64, "the staging assignment below");
+    const int sr = tid >> 2, sq = tid & 3;
+    const int stok = (tok0 + sr < ntok) ? tok0 + sr : ntok - 1;     // clamped: loads stay in bounds
+    const uint8_t * ga = qs + (size_t) (row0 + sr) * bpr * 16 + 32 * sq;             // + 16 kb0
+    const int8_t * gb = aqs + (size_t) stok * bpr * 32 + 64 * sq;                     // + 32 kb0
+    const _Float16 * gd = d + (size_t) (row0 + (tid & 63)) * bpr;                     // + kb0 (tid < 64)
+    const float2 * gs = asc + (size_t) stok * bpr + 2 * sq;                           // + kb0
+    // named registers, not arrays: a captured array stays in private memory
+    uint4 ra0, ra1, rb0, rb1, rb2, rb3, rd = make_uint4(0, 0, 0, 0), rs;
+    auto fetch = [&](int kb0) {
+        ra0 = *(const uint4 *) (ga + 16 * kb0);
+        ra1 = *(const uint4 *) (ga + 16 * kb0 + 16);
+        rb0 = *(const uint4 *) (gb + 32 * kb0);
+        rb1 = *(const uint4 *) (gb + 32 * kb0 + 16);
+        rb2 = *(const uint4 *) (gb + 32 * kb0 + 32);
+        rb3 = *(const uint4 *) (gb + 32 * kb0 + 48);
+        if (tid < 64) rd = *(const uint4 *) (gd + kb0);
+        rs = *(const uint4 *) (gs + kb0);
+    };
+    auto stash = [&](PfgStage & S) {
+        *(uint4 *) (S.a + sr * PFG_AP + 32 * sq) = ra0;
+        *(uint4 *) (S.a + sr * PFG_AP + 32 * sq + 16) = ra1;
+        *(uint4 *) (S.b + sr * PFG_BP + 64 * sq) = rb0;
+        *(uint4 *) (S.b + sr * PFG_BP + 64 * sq + 16) = rb1;
+        *(uint4 *) (S.b + sr * PFG_BP + 64 * sq + 32) = rb2;
+        *(uint4 *) (S.b + sr * PFG_BP + 64 * sq + 48) = rb3;
+        if (tid < 64) {
+            const unsigned dv0 = rd.x, dv1 = rd.y, dv2 = rd.z, dv3 = rd.w;
+            S.d[0][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv0 & 0xffff));
+            S.d[1][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv0 >> 16));
+            S.d[2][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv1 & 0xffff));
+            S.d[3][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv1 >> 16));
+            S.d[4][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv2 & 0xffff));
+            S.d[5][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv2 >> 16));
+            S.d[6][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv3 & 0xffff));
+            S.d[7][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv3 >> 16));
+        }
+        S.s[2 * sq][sr]     = make_float2(__uint_as_float(rs.x), __uint_as_float(rs.y));
+        S.s[2 * sq + 1][sr] = make_float2(__uint_as_float(rs.z), __uint_as_float(rs.w));
+    };
 
     const int mb = 0x4B400000;
     const lk_i4g seed = { mb, mb, mb, mb };
+    const int sh = 4 * (kg >> 1);                      // low or high nibbles
     lk_f4g acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = (lk_f4g){ 0.f, 0.f, 0.f, 0.f };
 
-    for (int kb0 = 0; kb0 < bpr; kb0 += PFG_KC) {
-        const int nk = (bpr - kb0 < PFG_KC) ? bpr - kb0 : PFG_KC;
-        __syncthreads();                                   // the previous chunk's scales are consumed
-        for (int e = tid; e < nk * PFG_BM; e += 256) {     // d4: coalesced along the row's blocks
-            const int r = e / nk, b = e % nk;
-            s_d[b][r] = d[(size_t) (row0 + r) * bpr + kb0 + b];
-        }
-        for (int e = tid; e < nk * PFG_BN; e += 256) {
-            const int t = e / nk, b = e % nk;
-            const int tc = (tok0 + t < ntok) ? tok0 + t : ntok - 1;
-            s_s[b][t] = asc[(size_t) tc * bpr + kb0 + b];
-        }
+    const int nck = bpr / PFG_KC;
+    fetch(0);
+    for (int ck = 0; ck < nck; ++ck) {
+        PfgStage & S = stg[ck & 1];
+        stash(S);                                      // stage ck&1 was last read two chunks ago
         __syncthreads();
-        for (int b0 = 0; b0 < nk; b0 += PFG_AHEAD) {
-            // operands of up to PFG_AHEAD blocks, all loads first
-            uint2 a8[PFG_AHEAD][2];
-            long b8[PFG_AHEAD][2];
+        if (ck + 1 < nck) fetch((ck + 1) * PFG_KC);    // the next chunk streams in during this one
+#pragma unroll 2
+        for (int b = 0; b < PFG_KC; ++b) {
+            long a[2], bv[2];
 #pragma unroll
-            for (int u = 0; u < PFG_AHEAD; ++u) {
-                const int b = kb0 + ((b0 + u < nk) ? b0 + u : b0);
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    a8[u][i] = *(const uint2 *) (ap[i] + (size_t) b * 16);
-                    b8[u][i] = *(const long *) (bp[i] + (size_t) b * 32);
-                }
+            for (int i = 0; i < 2; ++i) {
+                const uint2 q = *(const uint2 *) (S.a + (wr + 16 * i + l16) * PFG_AP + 16 * b + 8 * (kg & 1));
+                const uint32_t lo = (q.x >> sh) & 0x0F0F0F0Fu, hi = (q.y >> sh) & 0x0F0F0F0Fu;
+                a[i] = (long) (((uint64_t) hi << 32) | lo);
+                bv[i] = *(const long *) (S.b + (wt + 16 * i + l16) * PFG_BP + 32 * b + 8 * kg);
             }
+            lk_f4g F[2][2];
 #pragma unroll
-            for (int u = 0; u < PFG_AHEAD; ++u) {
-                if (b0 + u >= nk) break;                   // wave-uniform
-                const int b = b0 + u;
-                long a[2];
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    F[i][j] = (PFG_ABL & 2) ? __builtin_bit_cast(lk_f4g, (lk_i4g){ (int) a[i], (int) bv[j], (int) (a[i] >> 32), mb })
+                                            : __builtin_bit_cast(lk_f4g, __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bv[j], seed, 0, 0, 0));
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float2 sv = S.s[b][wt + 16 * j + l16];
+                const float c = __builtin_fmaf(sv.x, MAGIC, sv.y);
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
-                    const uint32_t lo = (a8[u][i].x >> sh) & 0x0F0F0F0Fu, hi = (a8[u][i].y >> sh) & 0x0F0F0F0Fu;
-                    a[i] = (long) (((uint64_t) hi << 32) | lo);
-                }
-                lk_f4g F[2][2];
+                    // d4 of rows 4kg .. 4kg+3 of row tile i: one 8-byte read
+                    const uint2 dw = *(const uint2 *) &S.d[b][wr + 16 * i + 4 * kg];
+                    const float d4[4] = { (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x & 0xffff)),
+                                          (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x >> 16)),
+                                          (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.y & 0xffff)),
+                                          (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.y >> 16)) };
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        F[i][j] = __builtin_bit_cast(lk_f4g, __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b8[u][j], seed, 0, 0, 0));
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const float2 s = s_s[b][wt + 16 * j + l16];
-                    const float c = __builtin_fmaf(s.x, MAGIC, s.y);
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        // d4 of rows 4kg .. 4kg+3 of row tile i: one 8-byte read
-                        const uint2 dw = *(const uint2 *) &s_d[b][wr + 16 * i + 4 * kg];
-                        const float d4[4] = { (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x & 0xffff)),
-                                              (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x >> 16)),
-                                              (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.y & 0xffff)),
-                                              (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.y >> 16)) };
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            acc[i][j][e] = __builtin_fmaf(d4[e], __builtin_fmaf(s.x, F[i][j][e], -c), acc[i][j][e]);
-                    }
+                    for (int e = 0; e < 4; ++e)
+                        acc[i][j][e] = (PFG_ABL & 4) ? acc[i][j][e] + F[i][j][e]
+                                                     : __builtin_fmaf(d4[e], __builtin_fmaf(sv.x, F[i][j][e], -c), acc[i][j][e]);
                 }
             }
         }
+        __syncthreads();                               // stage ck&1 fully read before it is refilled
     }
     // epilogue: lane holds rows 4kg .. 4kg+3 of each row tile for token l16 of each token tile
 #pragma unroll
@@ -161,9 +192,9 @@ extern "C" int lk_pf_gemm_q4_0(const void * qs, const void * d, int N, int bpr, 
     if (N < 0 || ntok < 0 || bpr < 1)
         return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: N %d / ntok %d / bpr %d", N, ntok, bpr);
     if (N == 0 || ntok == 0) return 0;
-    if (N % PFG_BM != 0 || out_ld % 4 != 0 || out_ld < N)
-        return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: N %d must be a multiple of %d, out_ld %d a multiple of 4 and >= N",
-                       N, PFG_BM, out_ld);
+    if (N % PFG_BM != 0 || bpr % PFG_KC != 0 || out_ld % 4 != 0 || out_ld < N)
+        return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: N %d must be a multiple of %d, bpr %d of %d, out_ld %d a multiple of 4 and >= N",
+                       N, PFG_BM, bpr, PFG_KC, out_ld);
     if (!qs || !d || !aqs || !asc || !out)
         return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: null pointer argument");
     if (((uintptr_t) qs & 15) || ((uintptr_t) d & 1) || ((uintptr_t) aqs & 7) || ((uintptr_t) asc & 7) ||

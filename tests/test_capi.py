@@ -97,6 +97,7 @@ def test_host_argument_errors():
     assert lib.lk_pf_gemm_q4_0(p, p, 100, 64, p, p, 4, None, p, 128, 0, None) == 1   # N % 64
     assert lib.lk_pf_gemm_q4_0(p, p, 128, 64, p, p, 4, None, p, 64, 0, None) == 1    # out_ld < N
     assert lib.lk_pf_gemm_q4_0(p, p, 128, 0, p, p, 4, None, p, 128, 0, None) == 1    # bpr < 1
+    assert lib.lk_pf_gemm_q4_0(p, p, 128, 12, p, p, 4, None, p, 128, 0, None) == 1   # bpr % 8
     assert lib.lk_pf_gemm_q4_0(p, None, 128, 64, p, p, 4, None, p, 128, 0, None) == 1  # null d
     assert lib.lk_pf_gemm_q4_0(q, p, 128, 64, p, p, 4, None, p, 128, 0, None) == 1   # qs misaligned
     assert lib.lk_pf_gemm_q4_0(None, None, 128, 64, None, None, 0, None, None, 128, 0, None) == 0  # no tokens

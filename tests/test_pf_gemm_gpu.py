@@ -4,7 +4,7 @@ the GPU, through the C ABI.
 The kernel accumulates every (token, row) over the blocks in order with the
 reference's fma sequence (k_pf_mmq, PF_EPI2), so every case is checked bit for
 bit against the oracle: the attention-output shape (2048 x 2048) and others
-(K staged in several LDS chunks, token counts off the 64-token tile, the
+(K staged in several LDS chunks of 8 blocks, token counts off the 64-token tile, the
 residual add, the per-token scale), and the chain from lk_pf_attn8_q81's
 planar Q8_1 output -- also against the float64 product of the dequantised
 weights and the float64 attention output as a sanity bound.
@@ -32,7 +32,7 @@ def _run(lk, qs, d, N, bpr, aqs, asc, ntok, out0, add, scale):
     return host(out)
 
 
-SHAPES = [(2048, 64, 256), (128, 64, 100), (64, 1, 1), (192, 70, 65), (64, 33, 3), (256, 96, 130)]
+SHAPES = [(2048, 64, 256), (128, 64, 100), (64, 8, 1), (192, 72, 65), (64, 16, 3), (256, 96, 130)]
 
 
 @pytest.mark.parametrize("N,bpr,ntok", SHAPES, ids=[f"N{a}_b{b}_t{c}" for a, b, c in SHAPES])
