@@ -19,30 +19,32 @@
 // so does the reference's main loop.  Its nvcc build may contract the
 // epilogue's acc * scale + out into one fma, a difference of one rounding.
 //
-// MI355X design: workgroup = 64 weight rows x 64 tokens, 4 waves of 32 x 32,
-// each a 2 x 2 grid of 16 x 16 v_mfma_i32_16x16x32_i8 tiles -- one 32-element
-// Q4_0 block per MFMA, because the scales change from block to block.  A
-// operand: lane l supplies weight row l%16, elements 8(l/16)..+7, i.e. the low
-// or high nibbles of bytes 0-7 or 8-15 of the 16-byte block (one shift, one
-// mask); B operand: 8 int8 of the activation row.  The accumulator is seeded
-// with 0x4B400000 so the integer sum arrives as the float F.  Staging: 8 blocks
-// at a time of the weight quants, the activation quants, the fp16 weight
-// scales and the (d8, 8 sum) token scales go through LDS in two stages (each
-// thread one 16-byte-coalesced quarter-row of each plane; the next stage's
-// global loads are in flight while the current one is computed); rows are
-// padded by 16 bytes, the scales kept as [block][row] and [block][token], so a
-// lane reads its 4 rows' d4 as one 8-byte read.  Loading the operands straight
-// from L2 instead (8 scattered bytes per lane) measured 240 us against 95 us
-// for C4's 4096 x 2048 x 2048.  The output tile is written as float4 (4
-// consecutive rows of one token).  Needs bpr % 8 == 0, as the reference's
-// pf_gemm_dense does.
+// MI355X design: workgroup = 64 weight rows x 128 tokens, 4 waves of 32 rows
+// x 64 tokens, each a 2 x 4 grid of 16 x 16 v_mfma_i32_16x16x32_i8 tiles --
+// one 32-element Q4_0 block per MFMA, because the scales change from block to
+// block.  A operand: lane l supplies weight row l%16, elements 8(l/16)..+7,
+// i.e. the low or high nibbles of bytes 0-7 or 8-15 of the 16-byte block (one
+// shift, one mask); B operand: 8 int8 of the activation row.  The accumulator
+// is seeded with 0x4B400000 so the integer sum arrives as the float F.
+// Staging: 4 blocks at a time of the weight quants, the activation quants, the
+// fp16 weight scales and the (d8, 8 sum) token scales go through LDS in two
+// stages (16-byte coalesced global loads; the next stage's loads are in flight
+// while the current one is computed); rows are padded (conflict-free 8-byte
+// operand reads), the scales kept as [block][row] and [block][token], so a
+// lane reads its 4 rows' d4 as one 8-byte read.  53 KB of LDS: 3 workgroups
+// per CU.  Measured on C4's 4096 x 2048 x 2048: operands straight from L2 (8
+// scattered bytes per lane) 240 us, LDS staging at a 32 x 32 wave tile 95 us,
+// this tiling 87 us.  The output tile is written as float4 (4 consecutive
+// rows of one token).  Needs bpr % 8 == 0, as the reference's pf_gemm_dense
+// does.
 #include "lk_common.h"
 
 #define PFG_BM 64                  // weight rows per workgroup
-#define PFG_BN 64                  // tokens per workgroup
-#define PFG_KC 8                   // blocks per LDS stage (the staging below moves exactly 8)
+#define PFG_BN 128                 // tokens per workgroup
+#define PFG_KC 4                   // blocks per LDS stage (the staging below moves exactly 4)
+#define PFG_TJ 4                   // 16-token tiles per wave
 #define PFG_AP (PFG_KC * 16 + 16)  // LDS pitch of a weight row (bytes, padded)
-#define PFG_BP (PFG_KC * 32 + 16)  // LDS pitch of an activation row
+#define PFG_BP (PFG_KC * 32 + 8)   // LDS pitch of an activation row (8-byte pad: 3 workgroups fit per CU)
 #ifndef PFG_ABL
 #define PFG_ABL 0                  // measurement builds only: 2 no MFMA, 4 no fma epilogue
 #endif
@@ -58,7 +60,7 @@ struct alignas(16) PfgStage {
 };
 
 template <bool ADD>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(256, 3)
 lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__ d, int N, int bpr,
                   const int8_t * __restrict__ aqs, const float2 * __restrict__ asc, int ntok,
                   const float * __restrict__ scale, float * __restrict__ out, int out_ld) {
@@ -67,60 +69,59 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = blockIdx.x * PFG_BM, tok0 = blockIdx.y * PFG_BN;
-    const int wr = (w & 1) * 32, wt = (w >> 1) * 32;   // the wave's 32 x 32 sub-tile
+    const int wr = (w & 1) * 32, wt = (w >> 1) * 64;   // the wave's 32 x 64 sub-tile
     const int l16 = lane & 15, kg = lane >> 4;
     constexpr float MAGIC = 12582912.0f;               // 1.5 * 2^23 = float bits 0x4B400000
 
-    // ---- staging: thread t moves row / token t/4, quarter t%4 of each plane --
-    static_assert(PFG_KC == 8 && PFG_BM == 64 && PFG_BN == 64, "the staging assignment below");
-    const int sr = tid >> 2, sq = tid & 3;
-    const int stok = (tok0 + sr < ntok) ? tok0 + sr : ntok - 1;     // clamped: loads stay in bounds
-    const uint8_t * ga = qs + (size_t) (row0 + sr) * bpr * 16 + 32 * sq;             // + 16 kb0
-    const int8_t * gb = aqs + (size_t) stok * bpr * 32 + 64 * sq;                     // + 32 kb0
+    // ---- staging (4 blocks per stage): thread t moves weight row t/4 (16 of
+    // its 64 bytes), token t/2 (64 of its 128 quant bytes, 2 of its 4 scale
+    // pairs) and, for t < 64, the 4 fp16 scales of weight row t
+    static_assert(PFG_KC == 4 && PFG_BM == 64 && PFG_BN == 128, "the staging assignment below");
+    const int ar = tid >> 2, aq = tid & 3, bt = tid >> 1, bq = tid & 1;
+    const int stok = (tok0 + bt < ntok) ? tok0 + bt : ntok - 1;     // clamped: loads stay in bounds
+    const uint8_t * ga = qs + (size_t) (row0 + ar) * bpr * 16 + 16 * aq;             // + 16 kb0
+    const int8_t * gb = aqs + (size_t) stok * bpr * 32 + 64 * bq;                     // + 32 kb0
     const _Float16 * gd = d + (size_t) (row0 + (tid & 63)) * bpr;                     // + kb0 (tid < 64)
-    const float2 * gs = asc + (size_t) stok * bpr + 2 * sq;                           // + kb0
+    const float2 * gs = asc + (size_t) stok * bpr + 2 * bq;                           // + kb0
     // named registers, not arrays: a captured array stays in private memory
-    uint4 ra0, ra1, rb0, rb1, rb2, rb3, rd = make_uint4(0, 0, 0, 0), rs;
+    uint4 ra0, rb0, rb1, rb2, rb3, rs;
+    uint2 rd = make_uint2(0, 0);
     auto fetch = [&](int kb0) {
         ra0 = *(const uint4 *) (ga + 16 * kb0);
-        ra1 = *(const uint4 *) (ga + 16 * kb0 + 16);
         rb0 = *(const uint4 *) (gb + 32 * kb0);
         rb1 = *(const uint4 *) (gb + 32 * kb0 + 16);
         rb2 = *(const uint4 *) (gb + 32 * kb0 + 32);
         rb3 = *(const uint4 *) (gb + 32 * kb0 + 48);
-        if (tid < 64) rd = *(const uint4 *) (gd + kb0);
+        if (tid < 64) rd = *(const uint2 *) (gd + kb0);
         rs = *(const uint4 *) (gs + kb0);
     };
     auto stash = [&](PfgStage & S) {
-        *(uint4 *) (S.a + sr * PFG_AP + 32 * sq) = ra0;
-        *(uint4 *) (S.a + sr * PFG_AP + 32 * sq + 16) = ra1;
-        *(uint4 *) (S.b + sr * PFG_BP + 64 * sq) = rb0;
-        *(uint4 *) (S.b + sr * PFG_BP + 64 * sq + 16) = rb1;
-        *(uint4 *) (S.b + sr * PFG_BP + 64 * sq + 32) = rb2;
-        *(uint4 *) (S.b + sr * PFG_BP + 64 * sq + 48) = rb3;
-        if (tid < 64) {
-            const unsigned dv0 = rd.x, dv1 = rd.y, dv2 = rd.z, dv3 = rd.w;
-            S.d[0][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv0 & 0xffff));
-            S.d[1][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv0 >> 16));
-            S.d[2][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv1 & 0xffff));
-            S.d[3][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv1 >> 16));
-            S.d[4][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv2 & 0xffff));
-            S.d[5][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv2 >> 16));
-            S.d[6][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv3 & 0xffff));
-            S.d[7][tid] = __builtin_bit_cast(_Float16, (unsigned short) (dv3 >> 16));
+        *(uint4 *) (S.a + ar * PFG_AP + 16 * aq) = ra0;
+        {   // 8-byte aligned rows: 8-byte stores
+            uint2 * pb = (uint2 *) (S.b + bt * PFG_BP + 64 * bq);
+            pb[0] = make_uint2(rb0.x, rb0.y); pb[1] = make_uint2(rb0.z, rb0.w);
+            pb[2] = make_uint2(rb1.x, rb1.y); pb[3] = make_uint2(rb1.z, rb1.w);
+            pb[4] = make_uint2(rb2.x, rb2.y); pb[5] = make_uint2(rb2.z, rb2.w);
+            pb[6] = make_uint2(rb3.x, rb3.y); pb[7] = make_uint2(rb3.z, rb3.w);
         }
-        S.s[2 * sq][sr]     = make_float2(__uint_as_float(rs.x), __uint_as_float(rs.y));
-        S.s[2 * sq + 1][sr] = make_float2(__uint_as_float(rs.z), __uint_as_float(rs.w));
+        if (tid < 64) {
+            S.d[0][tid] = __builtin_bit_cast(_Float16, (unsigned short) (rd.x & 0xffff));
+            S.d[1][tid] = __builtin_bit_cast(_Float16, (unsigned short) (rd.x >> 16));
+            S.d[2][tid] = __builtin_bit_cast(_Float16, (unsigned short) (rd.y & 0xffff));
+            S.d[3][tid] = __builtin_bit_cast(_Float16, (unsigned short) (rd.y >> 16));
+        }
+        S.s[2 * bq][bt]     = make_float2(__uint_as_float(rs.x), __uint_as_float(rs.y));
+        S.s[2 * bq + 1][bt] = make_float2(__uint_as_float(rs.z), __uint_as_float(rs.w));
     };
 
     const int mb = 0x4B400000;
     const lk_i4g seed = { mb, mb, mb, mb };
     const int sh = 4 * (kg >> 1);                      // low or high nibbles
-    lk_f4g acc[2][2];
+    lk_f4g acc[2][PFG_TJ];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = (lk_f4g){ 0.f, 0.f, 0.f, 0.f };
+        for (int j = 0; j < PFG_TJ; ++j) acc[i][j] = (lk_f4g){ 0.f, 0.f, 0.f, 0.f };
 
     const int nck = bpr / PFG_KC;
     fetch(0);
@@ -129,47 +130,52 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
         stash(S);                                      // stage ck&1 was last read two chunks ago
         __syncthreads();
         if (ck + 1 < nck) fetch((ck + 1) * PFG_KC);    // the next chunk streams in during this one
-#pragma unroll 2
+#pragma unroll
         for (int b = 0; b < PFG_KC; ++b) {
-            long a[2], bv[2];
+            long a[2], bv[PFG_TJ];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const uint2 q = *(const uint2 *) (S.a + (wr + 16 * i + l16) * PFG_AP + 16 * b + 8 * (kg & 1));
                 const uint32_t lo = (q.x >> sh) & 0x0F0F0F0Fu, hi = (q.y >> sh) & 0x0F0F0F0Fu;
                 a[i] = (long) (((uint64_t) hi << 32) | lo);
-                bv[i] = *(const long *) (S.b + (wt + 16 * i + l16) * PFG_BP + 32 * b + 8 * kg);
             }
-            lk_f4g F[2][2];
+#pragma unroll
+            for (int j = 0; j < PFG_TJ; ++j)
+                bv[j] = *(const long *) (S.b + (wt + 16 * j + l16) * PFG_BP + 32 * b + 8 * kg);
+            lk_f4g F[2][PFG_TJ];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < PFG_TJ; ++j)
                     F[i][j] = (PFG_ABL & 2) ? __builtin_bit_cast(lk_f4g, (lk_i4g){ (int) a[i], (int) bv[j], (int) (a[i] >> 32), mb })
                                             : __builtin_bit_cast(lk_f4g, __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bv[j], seed, 0, 0, 0));
+            // d4 of rows 4kg .. 4kg+3 of each row tile: one 8-byte read each
+            float d4[2][4];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int i = 0; i < 2; ++i) {
+                const uint2 dw = *(const uint2 *) &S.d[b][wr + 16 * i + 4 * kg];
+                d4[i][0] = (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x & 0xffff));
+                d4[i][1] = (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x >> 16));
+                d4[i][2] = (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.y & 0xffff));
+                d4[i][3] = (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.y >> 16));
+            }
+#pragma unroll
+            for (int j = 0; j < PFG_TJ; ++j) {
                 const float2 sv = S.s[b][wt + 16 * j + l16];
                 const float c = __builtin_fmaf(sv.x, MAGIC, sv.y);
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    // d4 of rows 4kg .. 4kg+3 of row tile i: one 8-byte read
-                    const uint2 dw = *(const uint2 *) &S.d[b][wr + 16 * i + 4 * kg];
-                    const float d4[4] = { (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x & 0xffff)),
-                                          (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x >> 16)),
-                                          (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.y & 0xffff)),
-                                          (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.y >> 16)) };
+                for (int i = 0; i < 2; ++i)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         acc[i][j][e] = (PFG_ABL & 4) ? acc[i][j][e] + F[i][j][e]
-                                                     : __builtin_fmaf(d4[e], __builtin_fmaf(sv.x, F[i][j][e], -c), acc[i][j][e]);
-                }
+                                                     : __builtin_fmaf(d4[i][e], __builtin_fmaf(sv.x, F[i][j][e], -c), acc[i][j][e]);
             }
         }
         __syncthreads();                               // stage ck&1 fully read before it is refilled
     }
     // epilogue: lane holds rows 4kg .. 4kg+3 of each row tile for token l16 of each token tile
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < PFG_TJ; ++j) {
         const int t = tok0 + wt + 16 * j + l16;
         if (t >= ntok) continue;
         const float sc = scale ? scale[t] : 1.0f;
@@ -192,9 +198,9 @@ extern "C" int lk_pf_gemm_q4_0(const void * qs, const void * d, int N, int bpr, 
     if (N < 0 || ntok < 0 || bpr < 1)
         return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: N %d / ntok %d / bpr %d", N, ntok, bpr);
     if (N == 0 || ntok == 0) return 0;
-    if (N % PFG_BM != 0 || bpr % PFG_KC != 0 || out_ld % 4 != 0 || out_ld < N)
+    if (N % PFG_BM != 0 || bpr % 8 != 0 || out_ld % 4 != 0 || out_ld < N)
         return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: N %d must be a multiple of %d, bpr %d of %d, out_ld %d a multiple of 4 and >= N",
-                       N, PFG_BM, bpr, PFG_KC, out_ld);
+                       N, PFG_BM, bpr, 8, out_ld);
     if (!qs || !d || !aqs || !asc || !out)
         return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: null pointer argument");
     if (((uintptr_t) qs & 15) || ((uintptr_t) d & 1) || ((uintptr_t) aqs & 7) || ((uintptr_t) asc & 7) ||
