@@ -19,10 +19,11 @@
 // so does the reference's main loop.  Its nvcc build may contract the
 // epilogue's acc * scale + out into one fma, a difference of one rounding.
 //
-// MI355X design: workgroup = 64 weight rows x 128 tokens, 4 waves of 32 rows
-// x 64 tokens, each a 2 x 4 grid of 16 x 16 v_mfma_i32_16x16x32_i8 tiles --
-// one 32-element Q4_0 block per MFMA, because the scales change from block to
-// block.  A operand: lane l supplies weight row l%16, elements 8(l/16)..+7,
+// MI355X design: workgroup = 128 weight rows x 128 tokens, 4 waves of 64
+// rows x 64 tokens, each a 4 x 4 grid of 16 x 16 v_mfma_i32_16x16x32_i8 tiles
+// -- one 32-element Q4_0 block per MFMA, because the scales change from block
+// to block; per token tile the 4 MFMAs go back to back, then their scale
+// epilogue.  A operand: lane l supplies weight row l%16, elements 8(l/16)..+7,
 // i.e. the low or high nibbles of bytes 0-7 or 8-15 of the 16-byte block (one
 // shift, one mask); B operand: 8 int8 of the activation row.  The accumulator
 // is seeded with 0x4B400000 so the integer sum arrives as the float F.
@@ -31,17 +32,19 @@
 // stages (16-byte coalesced global loads; the next stage's loads are in flight
 // while the current one is computed); rows are padded (conflict-free 8-byte
 // operand reads), the scales kept as [block][row] and [block][token], so a
-// lane reads its 4 rows' d4 as one 8-byte read.  53 KB of LDS: 3 workgroups
-// per CU.  Measured on C4's 4096 x 2048 x 2048: operands straight from L2 (8
-// scattered bytes per lane) 240 us, LDS staging at a 32 x 32 wave tile 95 us,
-// this tiling 87 us.  The output tile is written as float4 (4 consecutive
-// rows of one token).  Needs bpr % 8 == 0, as the reference's pf_gemm_dense
-// does.
+// lane reads its 4 rows' d4 as one 8-byte read.  64 KB of LDS, 213 VGPRs: 2
+// workgroups per CU.  Measured on C4's 4096 x 2048 x 2048: operands straight
+// from L2 (8 scattered bytes per lane) 240 us; LDS staging at a 32 x 32 wave
+// tile 95 us, 32 x 64 about 84 us, this 64 x 64 tile about 77 us.  The output
+// tile is written as float4 (4 consecutive rows of one token).  Needs
+// N % 128 == 0 and bpr % 8 == 0, as the reference's pf_gemm_dense does
+// (PF_BM = 128).
 #include "lk_common.h"
 
-#define PFG_BM 64                  // weight rows per workgroup
+#define PFG_BM 128                 // weight rows per workgroup
 #define PFG_BN 128                 // tokens per workgroup
 #define PFG_KC 4                   // blocks per LDS stage (the staging below moves exactly 4)
+#define PFG_TI 4                   // 16-row tiles per wave
 #define PFG_TJ 4                   // 16-token tiles per wave
 #define PFG_AP (PFG_KC * 16 + 16)  // LDS pitch of a weight row (bytes, padded)
 #define PFG_BP (PFG_KC * 32 + 8)   // LDS pitch of an activation row (8-byte pad: 3 workgroups fit per CU)
@@ -60,7 +63,7 @@ struct alignas(16) PfgStage {
 };
 
 template <bool ADD>
-__global__ void __launch_bounds__(256, 3)
+__global__ void __launch_bounds__(256, 2)
 lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__ d, int N, int bpr,
                   const int8_t * __restrict__ aqs, const float2 * __restrict__ asc, int ntok,
                   const float * __restrict__ scale, float * __restrict__ out, int out_ld) {
@@ -69,34 +72,36 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int row0 = blockIdx.x * PFG_BM, tok0 = blockIdx.y * PFG_BN;
-    const int wr = (w & 1) * 32, wt = (w >> 1) * 64;   // the wave's 32 x 64 sub-tile
+    const int wr = (w & 1) * 64, wt = (w >> 1) * 64;   // the wave's 64 x 64 sub-tile
     const int l16 = lane & 15, kg = lane >> 4;
     constexpr float MAGIC = 12582912.0f;               // 1.5 * 2^23 = float bits 0x4B400000
 
     // ---- staging (4 blocks per stage): thread t moves weight row t/4 (16 of
     // its 64 bytes), token t/2 (64 of its 128 quant bytes, 2 of its 4 scale
     // pairs) and, for t < 64, the 4 fp16 scales of weight row t
-    static_assert(PFG_KC == 4 && PFG_BM == 64 && PFG_BN == 128, "the staging assignment below");
-    const int ar = tid >> 2, aq = tid & 3, bt = tid >> 1, bq = tid & 1;
+    static_assert(PFG_KC == 4 && PFG_BM == 128 && PFG_BN == 128, "the staging assignment below");
+    const int ar = tid >> 1, aq = tid & 1, bt = tid >> 1, bq = tid & 1;
     const int stok = (tok0 + bt < ntok) ? tok0 + bt : ntok - 1;     // clamped: loads stay in bounds
-    const uint8_t * ga = qs + (size_t) (row0 + ar) * bpr * 16 + 16 * aq;             // + 16 kb0
+    const uint8_t * ga = qs + (size_t) (row0 + ar) * bpr * 16 + 32 * aq;             // + 16 kb0
     const int8_t * gb = aqs + (size_t) stok * bpr * 32 + 64 * bq;                     // + 32 kb0
-    const _Float16 * gd = d + (size_t) (row0 + (tid & 63)) * bpr;                     // + kb0 (tid < 64)
+    const _Float16 * gd = d + (size_t) (row0 + (tid & 127)) * bpr;                    // + kb0 (tid < 128)
     const float2 * gs = asc + (size_t) stok * bpr + 2 * bq;                           // + kb0
     // named registers, not arrays: a captured array stays in private memory
-    uint4 ra0, rb0, rb1, rb2, rb3, rs;
+    uint4 ra0, ra1, rb0, rb1, rb2, rb3, rs;
     uint2 rd = make_uint2(0, 0);
     auto fetch = [&](int kb0) {
         ra0 = *(const uint4 *) (ga + 16 * kb0);
+        ra1 = *(const uint4 *) (ga + 16 * kb0 + 16);
         rb0 = *(const uint4 *) (gb + 32 * kb0);
         rb1 = *(const uint4 *) (gb + 32 * kb0 + 16);
         rb2 = *(const uint4 *) (gb + 32 * kb0 + 32);
         rb3 = *(const uint4 *) (gb + 32 * kb0 + 48);
-        if (tid < 64) rd = *(const uint2 *) (gd + kb0);
+        if (tid < 128) rd = *(const uint2 *) (gd + kb0);
         rs = *(const uint4 *) (gs + kb0);
     };
     auto stash = [&](PfgStage & S) {
-        *(uint4 *) (S.a + ar * PFG_AP + 16 * aq) = ra0;
+        *(uint4 *) (S.a + ar * PFG_AP + 32 * aq) = ra0;
+        *(uint4 *) (S.a + ar * PFG_AP + 32 * aq + 16) = ra1;
         {   // 8-byte aligned rows: 8-byte stores
             uint2 * pb = (uint2 *) (S.b + bt * PFG_BP + 64 * bq);
             pb[0] = make_uint2(rb0.x, rb0.y); pb[1] = make_uint2(rb0.z, rb0.w);
@@ -104,7 +109,7 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
             pb[4] = make_uint2(rb2.x, rb2.y); pb[5] = make_uint2(rb2.z, rb2.w);
             pb[6] = make_uint2(rb3.x, rb3.y); pb[7] = make_uint2(rb3.z, rb3.w);
         }
-        if (tid < 64) {
+        if (tid < 128) {
             S.d[0][tid] = __builtin_bit_cast(_Float16, (unsigned short) (rd.x & 0xffff));
             S.d[1][tid] = __builtin_bit_cast(_Float16, (unsigned short) (rd.x >> 16));
             S.d[2][tid] = __builtin_bit_cast(_Float16, (unsigned short) (rd.y & 0xffff));
@@ -117,9 +122,9 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
     const int mb = 0x4B400000;
     const lk_i4g seed = { mb, mb, mb, mb };
     const int sh = 4 * (kg >> 1);                      // low or high nibbles
-    lk_f4g acc[2][PFG_TJ];
+    lk_f4g acc[PFG_TI][PFG_TJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < PFG_TI; ++i)
 #pragma unroll
         for (int j = 0; j < PFG_TJ; ++j) acc[i][j] = (lk_f4g){ 0.f, 0.f, 0.f, 0.f };
 
@@ -132,9 +137,9 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
         if (ck + 1 < nck) fetch((ck + 1) * PFG_KC);    // the next chunk streams in during this one
 #pragma unroll
         for (int b = 0; b < PFG_KC; ++b) {
-            long a[2], bv[PFG_TJ];
+            long a[PFG_TI], bv[PFG_TJ];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < PFG_TI; ++i) {
                 const uint2 q = *(const uint2 *) (S.a + (wr + 16 * i + l16) * PFG_AP + 16 * b + 8 * (kg & 1));
                 const uint32_t lo = (q.x >> sh) & 0x0F0F0F0Fu, hi = (q.y >> sh) & 0x0F0F0F0Fu;
                 a[i] = (long) (((uint64_t) hi << 32) | lo);
@@ -142,17 +147,10 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
 #pragma unroll
             for (int j = 0; j < PFG_TJ; ++j)
                 bv[j] = *(const long *) (S.b + (wt + 16 * j + l16) * PFG_BP + 32 * b + 8 * kg);
-            lk_f4g F[2][PFG_TJ];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < PFG_TJ; ++j)
-                    F[i][j] = (PFG_ABL & 2) ? __builtin_bit_cast(lk_f4g, (lk_i4g){ (int) a[i], (int) bv[j], (int) (a[i] >> 32), mb })
-                                            : __builtin_bit_cast(lk_f4g, __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bv[j], seed, 0, 0, 0));
             // d4 of rows 4kg .. 4kg+3 of each row tile: one 8-byte read each
-            float d4[2][4];
+            float d4[PFG_TI][4];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < PFG_TI; ++i) {
                 const uint2 dw = *(const uint2 *) &S.d[b][wr + 16 * i + 4 * kg];
                 d4[i][0] = (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x & 0xffff));
                 d4[i][1] = (float) __builtin_bit_cast(_Float16, (unsigned short) (dw.x >> 16));
@@ -161,14 +159,20 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
             }
 #pragma unroll
             for (int j = 0; j < PFG_TJ; ++j) {
+                // the 4 MFMAs of this token tile back to back, then their scale epilogue
+                lk_f4g F[PFG_TI];
+#pragma unroll
+                for (int i = 0; i < PFG_TI; ++i)
+                    F[i] = (PFG_ABL & 2) ? __builtin_bit_cast(lk_f4g, (lk_i4g){ (int) a[i], (int) bv[j], (int) (a[i] >> 32), mb })
+                                         : __builtin_bit_cast(lk_f4g, __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bv[j], seed, 0, 0, 0));
                 const float2 sv = S.s[b][wt + 16 * j + l16];
                 const float c = __builtin_fmaf(sv.x, MAGIC, sv.y);
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                for (int i = 0; i < PFG_TI; ++i)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        acc[i][j][e] = (PFG_ABL & 4) ? acc[i][j][e] + F[i][j][e]
-                                                     : __builtin_fmaf(d4[i][e], __builtin_fmaf(sv.x, F[i][j][e], -c), acc[i][j][e]);
+                        acc[i][j][e] = (PFG_ABL & 4) ? acc[i][j][e] + F[i][e]
+                                                     : __builtin_fmaf(d4[i][e], __builtin_fmaf(sv.x, F[i][e], -c), acc[i][j][e]);
             }
         }
         __syncthreads();                               // stage ck&1 fully read before it is refilled
@@ -180,7 +184,7 @@ lk_k_pf_gemm_q4_0(const uint8_t * __restrict__ qs, const _Float16 * __restrict__
         if (t >= ntok) continue;
         const float sc = scale ? scale[t] : 1.0f;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < PFG_TI; ++i) {
             float4 * p = (float4 *) (out + (size_t) t * out_ld + row0 + wr + 16 * i + 4 * kg);
             float4 v = make_float4(acc[i][j][0] * sc, acc[i][j][1] * sc, acc[i][j][2] * sc, acc[i][j][3] * sc);
             if (ADD) {

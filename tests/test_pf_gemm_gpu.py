@@ -32,7 +32,7 @@ def _run(lk, qs, d, N, bpr, aqs, asc, ntok, out0, add, scale):
     return host(out)
 
 
-SHAPES = [(2048, 64, 256), (128, 64, 100), (64, 8, 1), (192, 72, 65), (64, 16, 3), (256, 96, 130)]
+SHAPES = [(2048, 64, 256), (128, 64, 100), (128, 8, 1), (384, 72, 65), (128, 16, 3), (256, 96, 130)]
 
 
 @pytest.mark.parametrize("N,bpr,ntok", SHAPES, ids=[f"N{a}_b{b}_t{c}" for a, b, c in SHAPES])
