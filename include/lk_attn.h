@@ -90,6 +90,20 @@ int lk_attn_decode(const float * q, const void * kc, const void * vc,
                    const int * d_pos, float * part, float * out,
                    lk_block_q8_1 * yq8, void * stream);
 
+/* Allocation-free lk_attn_decode.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory or take a workspace (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * slice partials live in a static device array of the library, one per GPU,
+ * of the fixed size lk_attn_part_bytes() (2.2 MB: one record per query head
+ * and slot, the most any sequence length uses), held until the process ends;
+ * nothing is allocated at call time.  Same kernels and bit-identical results
+ * as lk_attn_decode.  Every call on a GPU shares that GPU's array, so calls
+ * that overlap in time on one GPU (different streams or threads) race; calls
+ * ordered on one stream do not. */
+int lk_attn_decode_noalloc(const float * q, const void * kc, const void * vc,
+                           const int * d_pos, float * out, lk_block_q8_1 * yq8,
+                           void * stream);
+
 /* Replaces k_attention_decode (reference kernels.cuh:653-658,
  * kernels.cu:768-852): one workgroup per query head, a cross-check only.
  * Like the reference it only serves seq <= 8192; for longer sequences it

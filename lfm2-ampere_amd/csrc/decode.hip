@@ -24,6 +24,7 @@
 //     run-to-run bit-identical) and optionally emits Q8_1 blocks.
 #include "lk_common.h"
 #include <math.h>
+#include <mutex>
 
 // fp32 -> (hi, lo) fp16 pair with hi + lo == x to 22 bits.  x - (float)hi is
 // exact in fp32 (hi is x rounded to 11 significant bits).
@@ -552,6 +553,59 @@ extern "C" int lk_attn_decode(const float * q, const void * kc, const void * vc,
     int e = lk_attn_split(q, kc, vc, d_pos, part, stream);
     if (e) return e;
     return lk_attn_combine(part, d_pos, out, yq8, stream);
+}
+
+// ---- allocation-free decode ------------------------------------------------
+// lk_attn_decode_noalloc keeps the slice partials in this file-scope device
+// array instead of a caller buffer.  Its size is fixed: one record per (query
+// head, slot), LK_N_HEADS x LK_ATTN_SPLIT x LK_ATTN_PARTW floats (2.2 MB), the
+// most any sequence length uses (the slice count is capped at LK_ATTN_SPLIT).
+// Each device holds its own copy until the process ends.  In host code the
+// name `scratch` is a host-side stand-in, never a device address: the device
+// address is looked up once per device with hipGetSymbolAddress and only that
+// pointer is passed to kernels.
+#define LK_DEC_SCRATCH_FLOATS ((size_t) LK_N_HEADS * LK_ATTN_SPLIT * LK_ATTN_PARTW)
+static __device__ __align__(256) float scratch[LK_DEC_SCRATCH_FLOATS];
+
+static float * lk_dec_scratch_ptr(int & err) {
+    static std::mutex mu;
+    static float * ptr[LK_MAX_DEVICES] = {};
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= LK_MAX_DEVICES) {
+        err = lk_fail(e != hipSuccess ? (int) e : (int) hipErrorInvalidDevice,
+                      "lk_attn_decode_noalloc: no usable current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void * p = nullptr;
+        const hipError_t g = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (g != hipSuccess || !p) {
+            err = lk_fail(g != hipSuccess ? (int) g : (int) hipErrorInvalidSymbol,
+                          "lk_attn_decode_noalloc: scratch lookup on device %d: %s", dev, hipGetErrorString(g));
+            return nullptr;
+        }
+        ptr[dev] = (float *) p;
+    }
+    err = 0;
+    return ptr[dev];
+}
+
+extern "C" int lk_attn_decode_noalloc(const float * q, const void * kc, const void * vc,
+                                      const int * d_pos, float * out, lk_block_q8_1 * yq8,
+                                      void * stream) {
+    static_assert(LK_DEC_SCRATCH_FLOATS * sizeof(float) >= (size_t) LK_N_HEADS * LK_ATTN_SPLIT * LK_ATTN_PARTW * sizeof(float),
+                  "scratch holds one full partial set");
+    if (!q || !kc || !vc || !d_pos)
+        return lk_fail(hipErrorInvalidValue, "lk_attn_decode_noalloc: null pointer argument");
+    int err = 0;
+    float * part = lk_dec_scratch_ptr(err);
+    if (!part) return err;
+    hipStream_t st = lk_stream(stream);
+    int rc = lk_split_launch(q, kc, vc, d_pos, part, st);
+    if (rc) return rc;
+    return lk_combine_launch(part, d_pos, out, yq8, st);
 }
 
 extern "C" int lk_attention_decode(const float * q, const void * kc, const void * vc,

@@ -237,3 +237,5 @@ int lk_fail(int code, const char * fmt, ...);
 // hipGetLastError after a launch, mapped into lk_fail.
 int lk_launch_status(const char * what);
 static inline hipStream_t lk_stream(void * s) { return (hipStream_t) s; }
+// Devices whose per-device scratch addresses the host side caches.
+#define LK_MAX_DEVICES 64

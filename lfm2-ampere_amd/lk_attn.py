@@ -33,6 +33,7 @@ EXPORTS = (
     "lk_decode_step_graph_create", "lk_decode_graph_run",
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
     "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows", "lk_gemv_q4_0", "lk_pf_gemm_q4_0",
+    "lk_attn_decode_noalloc",
 )
 
 
@@ -65,6 +66,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_attn_split": ([P, P, P, P, P, P], I),
         "lk_attn_combine": ([P, P, P, P, P], I),
         "lk_attn_decode": ([P, P, P, P, P, P, P, P], I),
+        "lk_attn_decode_noalloc": ([P, P, P, P, P, P, P], I),
         "lk_attention_decode": ([P, P, P, P, P, P, P], I),
         "lk_decode_graph_create": ([I, P, P, P, P, P, P, P, P, P], I),
         "lk_decode_graph_launch": ([P, P], I),
@@ -158,6 +160,13 @@ def attn_combine(part, d_pos, out=None, yq8=None, stream=None) -> None:
 def attn_decode(q, kc, vc, d_pos, part, out=None, yq8=None, stream=None) -> None:
     _check(load().lk_attn_decode(_ptr(q), _ptr(kc), _ptr(vc), _ptr(d_pos), _ptr(part),
                                  _ptr(out), _ptr(yq8), _stream(stream)), "lk_attn_decode")
+
+
+def attn_decode_noalloc(q, kc, vc, d_pos, out=None, yq8=None, stream=None) -> None:
+    """lk_attn_decode without a `part` workspace: the library's static
+    per-device scratch holds the partials (calls overlapping on one GPU race)."""
+    _check(load().lk_attn_decode_noalloc(_ptr(q), _ptr(kc), _ptr(vc), _ptr(d_pos),
+                                         _ptr(out), _ptr(yq8), _stream(stream)), "lk_attn_decode_noalloc")
 
 
 def attention_decode(q, kc, vc, d_pos, out=None, yq8=None, stream=None) -> None:
