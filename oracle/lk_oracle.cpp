@@ -164,14 +164,23 @@ void lko_q8_row(const float * v, int8_t * dst, float * scale, float mul) {
 
 static const float LKO_L2E = 1.4426950408889634f;
 
-// The wave-wide sum of 64 fp32 lane values, xor-butterfly 32,16,8,4,2,1 as
-// lane 0 sees it -- the order the HIP quantiser reduces q.c in.
-static float lko_bfly64(const float * x) {
-    float s[64];
-    for (int i = 0; i < 64; ++i) s[i] = x[i];
-    for (int o = 32; o > 0; o >>= 1) {
-        float t[64];
-        for (int i = 0; i < 64; ++i) t[i] = s[i] + s[i ^ o];
+// q.c in the reference's order (prefill.cu:1279-1284): the row is held by a
+// 32-lane warp, two values per lane, so lane l first forms the pair sum
+// v[2l]*c[2l] + v[2l+1]*c[2l+1] (each product rounded, then the add: the
+// source text, read without contraction -- nvcc's default -fmad=true may fuse
+// one of the products into an fma, a difference of at most one rounding of
+// the pair), then the xor butterfly over lanes with offsets 16, 8, 4, 2, 1;
+// lane 0's value is returned.
+static float lko_qc_ref(const float * v, const float * c) {
+    float s[32];
+    for (int l = 0; l < 32; ++l) {
+        const float a = v[2 * l] * c[2 * l];
+        const float b = v[2 * l + 1] * c[2 * l + 1];
+        s[l] = a + b;
+    }
+    for (int o = 16; o > 0; o >>= 1) {
+        float t[32];
+        for (int l = 0; l < 32; ++l) t[l] = s[l] + s[l ^ o];
         std::memcpy(s, t, sizeof s);
     }
     return s[0];
@@ -179,20 +188,16 @@ static float lko_bfly64(const float * x) {
 
 // Q quantiser (reference prefill.cu:1271-1287): every (token, head) row of qh
 // fp16 [m][2048] -> q8 int8 [m][2048], qsc [m][32] = d * log2(e),
-// qcs [m][32] = (q . c) * log2(e) with c = cm[head/4] (0 without cm).
-// The q.c sum is the lane-product v_d*c_d reduced by lko_bfly64.
+// qcs [m][32] = (q . c) * log2(e) with c = cm[head/4] (0 without cm), q.c
+// summed by lko_qc_ref.
 void lko_pf_q8(const uint16_t * qh, int m, const float * cm,
                int8_t * q8, float * qsc, float * qcs) {
-    float v[LKO_D], pr[LKO_D];
+    float v[LKO_D];
     for (int r = 0; r < m * LKO_H; ++r) {
         for (int d = 0; d < LKO_D; ++d) v[d] = lko_h2f(qh[(size_t) r * LKO_D + d]);
         lko_q8_row(v, q8 + (size_t) r * LKO_D, qsc + r, LKO_L2E);
         float qc = 0.0f;
-        if (cm) {
-            const float * c = cm + ((r % LKO_H) / LKO_G) * LKO_D;
-            for (int d = 0; d < LKO_D; ++d) pr[d] = v[d] * c[d];
-            qc = lko_bfly64(pr);
-        }
+        if (cm) qc = lko_qc_ref(v, cm + ((r % LKO_H) / LKO_G) * LKO_D);
         qcs[r] = qc * LKO_L2E;
     }
 }

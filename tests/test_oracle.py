@@ -198,6 +198,50 @@ def test_pf_q8_layout_and_scales(oracle):
             assert abs(qcs[t, h] - want) <= 1e-5 * (1 + abs(want))
 
 
+def _warp_qc_reference_order(row, c):
+    """q.c as the reference's k_pf_q8 computes it (prefill.cu:1279-1284),
+    simulated lane by lane in float32: lane l holds values 2l and 2l+1, forms
+    v[2l]*c[2l] + v[2l+1]*c[2l+1], then __shfl_xor_sync with offsets 16..1."""
+    f = np.float32
+    s = [f(f(row[2 * l] * c[2 * l]) + f(row[2 * l + 1] * c[2 * l + 1])) for l in range(32)]
+    o = 16
+    while o:
+        s = [f(s[l] + s[l ^ o]) for l in range(32)]
+        o >>= 1
+    return s[0]
+
+
+def _other_order_qc(row, c):
+    """The same sum in a different, plausible order (value strides 32 .. 1)."""
+    f = np.float32
+    s = [f(row[i] * c[i]) for i in range(64)]
+    o = 32
+    while o:
+        s = [f(s[i] + s[i ^ o]) for i in range(64)]
+        o >>= 1
+    return s[0]
+
+
+def test_pf_q8_qc_reference_order(oracle):
+    """qcs bit for bit against a lane-level simulation of the reference warp's
+    reduction; and the simulation tells the orders apart on these inputs (so
+    a kernel or oracle in another order would fail this test)."""
+    rng = np.random.default_rng(19)
+    m = 4
+    qh = (rng.standard_normal((m, 2048)) * 0.7).astype(np.float16)
+    cm = rng.standard_normal((8, 64)).astype(np.float32)
+    _, _, qcs = oracle.pf_q8(qh.view(np.uint16), m, cm)
+    l2e = np.float32(1.4426950408889634)
+    differ = 0
+    for t in range(m):
+        for h in range(32):
+            row = qh[t, h * 64:(h + 1) * 64].astype(np.float32)
+            want = _warp_qc_reference_order(row, cm[h // 4])
+            assert qcs[t, h].view(np.uint32) == np.float32(want * l2e).view(np.uint32), (t, h)
+            differ += _other_order_qc(row, cm[h // 4]) != want
+    assert differ > 0
+
+
 def test_pf_k8_layout_and_smoothing(oracle):
     rng = np.random.default_rng(10)
     S, kstride = 13, 16
