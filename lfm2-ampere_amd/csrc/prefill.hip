@@ -30,6 +30,7 @@
 #include <math.h>
 #include <algorithm>
 #include <type_traits>
+#include <mutex>
 
 // ---------------------------------------------------------------------------
 // int8 quantisers.  Eight lanes per 64-wide (row, head), eight consecutive
@@ -40,10 +41,12 @@
 // helpers (lk_q8_row8, lk_max8, lk_load8h) live in lk_common.h.
 
 // Q: qh fp16 [m][2048] -> q8 [m][2048], qsc [m][32] = d*log2(e), qcs [m][32] =
-// (q.c)*log2(e), or 0 without cm.  q.c = sum over d of v_d*c_d by the xor
-// butterfly over d with strides 32, 16, 8, 4, 2, 1 (fixed order): the first
-// three strides pair lanes of the group (xor 4, 2, 1), the last three pair
-// values inside a lane.
+// (q.c)*log2(e), or 0 without cm.  q.c is summed in the reference's order
+// (prefill.cu:1279-1284, a 32-lane warp with values 2l, 2l+1 in lane l): the
+// pair sums s_k = v[2k]*c[2k] + v[2k+1]*c[2k+1], then the butterfly over k with
+// offsets 16, 8, 4, 2, 1.  Here lane j of the 8-lane group holds pairs
+// k = 4j..4j+3, so offsets 16, 8, 4 are lane exchanges xor 4, 2, 1 and offsets
+// 2, 1 pair the lane's own sums: (s0 + s2) + (s1 + s3).
 __global__ void __launch_bounds__(256)
 lk_k_pf_q8(const _Float16 * __restrict__ qh, int m, const float * __restrict__ cm,
            int8_t * __restrict__ q8, float * __restrict__ qsc, float * __restrict__ qcs) {
@@ -56,16 +59,17 @@ lk_k_pf_q8(const _Float16 * __restrict__ qh, int m, const float * __restrict__ c
     float qc = 0.0f;
     if (cm) {
         const float * c = cm + ((r % LK_N_HEADS) / LK_G) * LK_HEAD_DIM + 8 * j;
-        float t[8];
+        float t[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = v[i] * c[i];
+        for (int i = 0; i < 4; ++i) {
+            const float a = v[2 * i] * c[2 * i], b = v[2 * i + 1] * c[2 * i + 1];
+            t[i] = a + b;
+        }
 #pragma unroll
         for (int o = 4; o > 0; o >>= 1)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) t[i] += __shfl_xor(t[i], o, 64);
-        const float u0 = t[0] + t[4], u1 = t[1] + t[5], u2 = t[2] + t[6], u3 = t[3] + t[7];
-        const float w0 = u0 + u2, w1 = u1 + u3;
-        qc = w0 + w1;
+            for (int i = 0; i < 4; ++i) t[i] += __shfl_xor(t[i], o, 64);
+        qc = (t[0] + t[2]) + (t[1] + t[3]);
     }
     if (j == 0) qcs[r] = qc * LK_LOG2E_F;
 }
@@ -898,20 +902,69 @@ extern "C" int lk_pf_split_override(int tiles) {
     return 0;
 }
 
-// Device address of the partial scratch, per device (looked up once).
-static float * pf_part_ptr(int & err) {
-    static float * ptr[64] = {};
+// Device address of the partial scratch, per device (looked up once), and the
+// guard of its single-stream use: the stream of the last splitting launch on
+// each device and an event recorded after its combine.  A splitting launch on
+// another stream while that event is still pending would overwrite partials
+// the earlier launch has not merged yet; it is refused (hipErrorNotReady)
+// instead.  Launches on one stream are ordered and always accepted.  Under
+// stream capture the guard is not applied (the graph's own order decides).
+struct PfScratchUse {
+    float * ptr = nullptr;
+    hipStream_t last = nullptr;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+};
+static std::mutex g_pf_mu;
+static PfScratchUse g_pf_use[LK_MAX_DEVICES];
+
+static float * pf_part_acquire(hipStream_t st, int & err, int & dev_out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess || dev < 0 || dev >= 64) { err = lk_fail(e != hipSuccess ? (int) e : (int) hipErrorInvalidDevice, "prefill: no current device"); return nullptr; }
-    if (!ptr[dev]) {
+    if (e != hipSuccess || dev < 0 || dev >= LK_MAX_DEVICES) {
+        err = lk_fail(e != hipSuccess ? (int) e : (int) hipErrorInvalidDevice, "prefill: no usable current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_pf_mu);
+    PfScratchUse & u = g_pf_use[dev];
+    if (!u.ptr) {
         void * p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_pf_part));
         if (e != hipSuccess) { err = lk_fail((int) e, "prefill: scratch lookup: %s", hipGetErrorString(e)); return nullptr; }
-        ptr[dev] = (float *) p;
+        e = hipEventCreateWithFlags(&u.done, hipEventDisableTiming);
+        if (e != hipSuccess) { err = lk_fail((int) e, "prefill: scratch guard event: %s", hipGetErrorString(e)); return nullptr; }
+        u.ptr = (float *) p;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    (void) hipStreamIsCapturing(st, &cs);
+    if (cs == hipStreamCaptureStatusNone && u.pending && u.last != st) {
+        e = hipEventQuery(u.done);
+        (void) hipGetLastError();                     // the query's status is not a launch error
+        if (e == hipErrorNotReady) {
+            err = lk_fail(hipErrorNotReady,
+                          "prefill: a split-K launch on another stream of device %d is still pending; "
+                          "split launches share one partial buffer per device: order them on one stream "
+                          "(or wait for the earlier one)", dev);
+            return nullptr;
+        }
     }
     err = 0;
-    return ptr[dev];
+    dev_out = dev;
+    return u.ptr;
+}
+
+// After the combine is enqueued on st: mark the scratch busy until it completes.
+static int pf_part_release(hipStream_t st, int dev) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    (void) hipStreamIsCapturing(st, &cs);
+    if (cs != hipStreamCaptureStatusNone) return 0;
+    std::lock_guard<std::mutex> lock(g_pf_mu);
+    PfScratchUse & u = g_pf_use[dev];
+    const hipError_t e = hipEventRecord(u.done, st);
+    if (e != hipSuccess) return lk_fail((int) e, "prefill: scratch guard record: %s", hipGetErrorString(e));
+    u.last = st;
+    u.pending = true;
+    return 0;
 }
 
 static int pf_slots_per_device() {
@@ -1064,8 +1117,8 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
                            (float *) nullptr);
         return lk_launch_status(what);
     }
-    int err = 0;
-    float * pbuf = pf_part_ptr(err);
+    int err = 0, dev = 0;
+    float * pbuf = pf_part_acquire(st, err, dev);
     if (!pbuf) return err;
     hipLaunchKernelGGL(lk_k_pf_attn<INT8>, dim3(wk.n_items * LK_N_KV_HEADS), dim3(256), 0, st,
                        q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk, pbuf);
@@ -1073,7 +1126,9 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
     if (rc) return rc;
     hipLaunchKernelGGL(lk_k_pf_combine, dim3(wk.n_split, LK_N_KV_HEADS, 2), dim3(256), 0, st,
                        (const float *) pbuf, m, P, wk, o, aqs, asc);
-    return lk_launch_status(what);
+    rc = lk_launch_status(what);
+    if (rc) return rc;
+    return pf_part_release(st, dev);
 }
 
 extern "C" int lk_pf_attn8_q81(const int8_t * q8, const float * qsc, const float * qcs,

@@ -261,12 +261,24 @@ def test_attn_auto_split(lk, oracle, m, P, near):
 
 # ---- BASELINE prefill configurations (sampled rows against the float64 oracle) -----------------
 def _config_rows(m, long_ctx):
-    rows = {0, 63, 64, 1023, m - 1} if long_ctx else \
-        {0, 1, 31, 32, 63, 64, 65, 127, 128, 1000, 1023, 1024, 2047, 2048, m // 2 + 17, m - 2, m - 1}
+    if long_ctx:
+        rows = {0, 63, 64, 1023, 2048, m - 1}
+    else:
+        # every 64-row block boundary (the kernel's query blocks, and so the
+        # split-K parts' edges), the 32-row exactness tiles around the window
+        # edge, and a seeded spread: 256+ rows in all
+        rows = {r for b in range(0, m, 64) for r in (b, b + 63) if r < m}
+        rows |= {1, 31, 32, 33, 65, 1000, 1023, 1024, 1025, 2047, 2048, m // 2 + 17, m - 2}
+        rows |= set(np.random.default_rng(4).choice(m, 96, replace=False).tolist())
     return np.array(sorted(r for r in rows if r < m), np.int32)
 
 
-def _config_check(lk, oracle, qh, kc, vc, P, m, near, sink):
+def _config_check(lk, oracle, qh, kc, vc, P, m, near, sink, pure_rows=None):
+    """The int8 kernel on chunk [P, P+m) of a prompt against the float64
+    restatement of the same int8 algorithm (2e-3); with pure_rows, also the
+    int8 kernel and the fp16 kernel against plain float64 attention on those
+    rows (the reference reports this error for its int8 scoring,
+    tests/test_prefill.cu:862-866), returned as (rel_rms, max_rel) pairs."""
     S = P + m
     kstride = lk.kstride_for(S)
     q8 = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
@@ -283,12 +295,28 @@ def _config_check(lk, oracle, qh, kc, vc, P, m, near, sink):
     rows = _config_rows(m, P > 0)
     Kh = host_h(kc[:S]).reshape(-1)
     Vh = host_h(vc[:S]).reshape(-1)
-    ref8 = oracle.pf_ref8(host(q8), host(qsc), host(qcs), host_h(qchunk), m, P, host(k8), host(ksc),
+    Qh = host_h(qchunk)
+    ref8 = oracle.pf_ref8(host(q8), host(qsc), host(qcs), Qh, m, P, host(k8), host(ksc),
                           kstride, Kh, Vh, near, sink, rows=rows)
     rel = oracle.rel_err(host(o), ref8)
     note(f"  rows {len(rows)}: rel vs same-algorithm float64 {rel:.3e}")
     assert rel <= 2e-3
     assert bool(torch.isfinite(o).all())
+    if pure_rows is None:
+        return None
+    o16 = torch.empty(m, 2048, device="cuda")
+    lk.pf_attn(qchunk, m, P, kc, vc, o16)
+    torch.cuda.synchronize()
+    pr = np.asarray(pure_rows, np.int32)
+    ref = oracle.pf_ref(Qh, m, P, Kh, Vh, rows=pr)[pr]
+    out = {}
+    for name, got in (("int8", host(o)[pr]), ("fp16", host(o16)[pr])):
+        e = got.astype(np.float64) - ref
+        out[name] = (float(np.sqrt(np.mean(e * e)) / np.sqrt(np.mean(ref * ref))),
+                     float(np.max(np.abs(e)) / np.max(np.abs(ref))))
+    note(f"  vs plain float64 attention on {len(pr)} rows: int8 rel-RMS {out['int8'][0]:.3e} "
+         f"max-rel {out['int8'][1]:.3e}; fp16 rel-RMS {out['fp16'][0]:.3e} max-rel {out['fp16'][1]:.3e}")
+    return out
 
 
 def test_config_c4(lk, oracle):
@@ -298,11 +326,23 @@ def test_config_c4(lk, oracle):
     _config_check(lk, oracle, qh, kc, vc, 0, S, 1024, 1)
 
 
-def test_config_c5_last_chunk(lk, oracle):
+@pytest.mark.parametrize("P", [65536, 126976], ids=["mid_chunk", "last_chunk"])
+def test_config_c5_chunk(lk, oracle, P):
+    """C5 (heavy-tailed Q/K with x20 outlier channels, the stress case of the
+    int8 scoring): a mid chunk and the last chunk against the same-algorithm
+    restatement, and the int8 error against plain float64 attention -- an
+    information figure in the reference (test_prefill.cu:862-866), bounded
+    loosely here, beside the fp16 kernel's error (held to 2e-3)."""
     import lk_configs
-    note("prefill config C5, last 4096 chunk at P=126976 (heavy-tailed Q/K)")
+    note(f"prefill config C5, 4096 chunk at P={P} (heavy-tailed Q/K)")
     qh, kc, vc, S = lk_configs.prefill_inputs("C5")
-    _config_check(lk, oracle, qh, kc, vc, S - 4096, 4096, 1024, 1)
+    err = _config_check(lk, oracle, qh, kc, vc, P, 4096, 1024, 1, pure_rows=[0, 1000, 2047, 3000, 4095])
+    assert err["fp16"][1] <= 2e-3
+    # int8 on these rows: about 0.1 rel-RMS (the x20 channels set every row's
+    # absmax scale, so the other 62 channels keep 1-3 int8 levels).  That is the
+    # reference algorithm's own error (the same-algorithm check above holds to
+    # 2e-3); the bound only catches a blow-up.
+    assert err["int8"][0] <= 0.3 and err["int8"][1] <= 2.0
 
 
 # ---- planar Q8_1 of the attention output (reference k_pf_quant_rows) ----------------------------
@@ -356,3 +396,34 @@ def test_attn_fused_q81_equals_quant_rows(lk, oracle, m, P, near, L, int8):
     assert torch.equal(aqs2, aqs) and torch.equal(asc2.view(torch.int32), asc.view(torch.int32))
     qso, sco = oracle.pf_quant_rows(host(o), m, 2048, 64)
     assert np.array_equal(host(aqs), qso) and np.array_equal(host(asc).view(np.uint32), sco.view(np.uint32))
+
+
+# ---- the shared split-K partial buffer: one stream at a time ----------------------------------
+def test_split_scratch_refuses_a_second_stream_while_pending(lk, oracle):
+    """Split launches share the library's partial buffer on a device.  A split
+    launch on stream B while one on stream A is still pending is refused with
+    hipErrorNotReady (600) and a message; once A has completed, B is accepted;
+    launches ordered on one stream are always accepted.  A's result is intact."""
+    m, P = 1024, 0
+    K, V, Q = _inputs(oracle, m, P)
+    d = _Dev(lk, K, V, Q, m, P, False)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    oa = torch.full((m, 2048), float("nan"), device="cuda")
+    ob = torch.full((m, 2048), float("nan"), device="cuda")
+    note("pf split scratch guard: two streams")
+    try:
+        lk.pf_split_override(2)                     # this chunk splits
+        with torch.cuda.stream(sa):
+            torch.cuda._sleep(200_000_000)          # keep stream A busy (about 0.1 s)
+        lk.pf_attn(d.qh, m, P, d.kc, d.vc, oa, stream=sa)
+        lk.pf_attn(d.qh, m, P, d.kc, d.vc, oa, stream=sa)          # same stream: accepted
+        with pytest.raises(lk.LkError) as ei:
+            lk.pf_attn(d.qh, m, P, d.kc, d.vc, ob, stream=sb)
+        assert "hipError 600" in str(ei.value) and "another stream" in str(ei.value)
+        sa.synchronize()
+        lk.pf_attn(d.qh, m, P, d.kc, d.vc, ob, stream=sb)          # A is done: accepted
+        sb.synchronize()
+    finally:
+        lk.pf_split_override(0)
+    assert np.array_equal(host(oa).view(np.uint32), host(ob).view(np.uint32))
+    assert oracle.rel_err(host(oa), oracle.pf_ref(Q, m, P, K, V)) <= 2e-3
