@@ -206,6 +206,7 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     // the interface: split q = hi + lo (fp16 x fp16 products are exact in fp32)
     // and both halves are multiplied.
     lk_h8 qbh[2], qbl[2];
+    int qsh = 0;                                            // q of this lane's head is scaled by 2^-qsh
     {
         const int qrow = (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
         const float * qp = (FUSED ? pr.q_src : q) + qrow;
@@ -222,6 +223,22 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
                 *(lk_f4 *) (qo + 36) = (lk_f4){ hi[4], hi[5], hi[6], hi[7] };
             }
         }
+        // The fp16 hi half of q must be finite: a head whose largest |q| reaches
+        // 2^15 is scaled by 2^-k first (exact) so that it stays below 2^15, and
+        // its scores are scaled back by 2^k below.  k = 0 for every other head
+        // (the usual case, RMS-normed q), which leaves the arithmetic untouched.
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) am = fmaxf(am, fmaxf(fabsf(lo[i]), fabsf(hi[i])));
+        am = lk_xrow_max(am);                               // the head's 64 dims (lanes ^16, ^32)
+        int e2 = 0;
+        if (am >= 32768.0f && am <= 3.4e38f) {              // finite and too large for the fp16 split
+            (void) frexpf(am, &e2);                         // am < 2^e2
+            e2 -= 15;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { lo[i] = ldexpf(lo[i], -e2); hi[i] = ldexpf(hi[i], -e2); }
+        }
+        qsh = e2;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             _Float16 h, l;
@@ -229,7 +246,8 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
             lk_split_h(hi[i], h, l); qbh[1][i] = h; qbl[1][i] = l;
         }
     }
-    const float SC = 0.125f * LK_LOG2E_F;      // scores in log2 units
+    // scores in log2 units; the power-of-2 factor undoes the q scaling above
+    const float SC = ldexpf(0.125f * LK_LOG2E_F, qsh);
     // Running max is raised only when a score exceeds it by 2^8 in p: P stays
     // far inside fp16 range and most tiles skip the rescale.
     constexpr float HEADROOM = 8.0f;

@@ -101,6 +101,28 @@ def test_constant_keys_average(lk, oracle):
     assert abs_err(host(out), want) <= 1e-5
 
 
+def test_large_q_heads(lk, oracle):
+    """q is fp32 in the interface; heads whose |q| reaches past fp16's range
+    (the kernel's q = hi + lo fp16 split) are scaled by a power of 2 inside the
+    kernel.  Mixed in one kv group with ordinary heads, against float64."""
+    rng = np.random.default_rng(29)
+    seq = 5000
+    q = rng.standard_normal((32, 64)).astype(np.float32)
+    q[1] *= 4e4                 # max |q| ~ 1e5 > 65504
+    q[6] *= 1e9                 # one-hot softmax
+    q[13] *= 3e4
+    kc = (rng.standard_normal((seq, 8, 64)) * 2.5e-4).astype(np.float16)
+    kc[:, 1] *= 4000.0          # kv head 1 (heads 4-7) at ordinary scale
+    vc = rng.standard_normal((seq, 8, 64)).astype(np.float16)
+    note("decode large-|q| heads")
+    out, _ = _run_decode(lk, dev(q), dev_h(kc.view(np.uint16)), dev_h(vc.view(np.uint16)), seq)
+    ref = oracle.decode_ref(q, kc.view(np.uint16), vc.view(np.uint16), seq)
+    o = host(out)
+    assert np.isfinite(o).all()
+    for h in range(32):
+        assert oracle.rel_err(o[h], ref[h]) <= 2e-3, h
+
+
 def test_bitwise_deterministic(lk, oracle):
     rng = np.random.default_rng(23)
     seq = 77777
