@@ -47,7 +47,7 @@
 #define PFG_TI 4                   // 16-row tiles per wave
 #define PFG_TJ 4                   // 16-token tiles per wave
 #define PFG_AP (PFG_KC * 16 + 16)  // LDS pitch of a weight row (bytes, padded)
-#define PFG_BP (PFG_KC * 32 + 8)   // LDS pitch of an activation row (8-byte pad: 3 workgroups fit per CU)
+#define PFG_BP (PFG_KC * 32 + 8)   // LDS pitch of an activation row (bytes; the 8-byte pad spreads the rows over the banks)
 #ifndef PFG_ABL
 #define PFG_ABL 0                  // measurement builds only: 2 no MFMA, 4 no fma epilogue
 #endif
@@ -207,9 +207,10 @@ extern "C" int lk_pf_gemm_q4_0(const void * qs, const void * d, int N, int bpr, 
                        N, PFG_BM, bpr, 8, out_ld);
     if (!qs || !d || !aqs || !asc || !out)
         return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: null pointer argument");
-    if (((uintptr_t) qs & 15) || ((uintptr_t) d & 1) || ((uintptr_t) aqs & 7) || ((uintptr_t) asc & 7) ||
+    // the widths the kernel loads and stores at: qs, aqs, asc and out 16 bytes, d 8 bytes, scale 4
+    if (((uintptr_t) qs & 15) || ((uintptr_t) d & 7) || ((uintptr_t) aqs & 15) || ((uintptr_t) asc & 15) ||
         ((uintptr_t) out & 15) || ((uintptr_t) scale & 3))
-        return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: misaligned argument (qs 16 B, out 16 B, aqs / asc 8 B)");
+        return lk_fail(hipErrorInvalidValue, "lk_pf_gemm_q4_0: misaligned argument (qs, aqs, asc, out 16 B; d 8 B; scale 4 B)");
     const dim3 grid(N / PFG_BM, (ntok + PFG_BN - 1) / PFG_BN);
     const hipStream_t st = lk_stream(stream);
     if (add)

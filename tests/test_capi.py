@@ -100,6 +100,11 @@ def test_host_argument_errors():
     assert lib.lk_pf_gemm_q4_0(p, p, 128, 12, p, p, 4, None, p, 128, 0, None) == 1   # bpr % 8
     assert lib.lk_pf_gemm_q4_0(p, None, 128, 64, p, p, 4, None, p, 128, 0, None) == 1  # null d
     assert lib.lk_pf_gemm_q4_0(q, p, 128, 64, p, p, 4, None, p, 128, 0, None) == 1   # qs misaligned
+    # every operand is checked at the width the kernel loads it with
+    assert lib.lk_pf_gemm_q4_0(p, ctypes.c_void_p(0x1004), 128, 64, p, p, 4, None, p, 128, 0, None) == 1  # d: 8 B
+    assert lib.lk_pf_gemm_q4_0(p, p, 128, 64, q, p, 4, None, p, 128, 0, None) == 1   # aqs: 16 B
+    assert lib.lk_pf_gemm_q4_0(p, p, 128, 64, p, q, 4, None, p, 128, 0, None) == 1   # asc: 16 B
+    assert b"misaligned" in lib.lk_last_error()
     assert lib.lk_pf_gemm_q4_0(None, None, 128, 64, None, None, 0, None, None, 128, 0, None) == 0  # no tokens
 
 

@@ -4,7 +4,7 @@ the GPU, through the C ABI.
 The kernel accumulates every (token, row) over the blocks in order with the
 reference's fma sequence (k_pf_mmq, PF_EPI2), so every case is checked bit for
 bit against the oracle: the attention-output shape (2048 x 2048) and others
-(K staged in several LDS chunks of 8 blocks, token counts off the 64-token tile, the
+(K staged through LDS 4 blocks per stage, token counts off the 128-token workgroup tile, the
 residual add, the per-token scale), and the chain from lk_pf_attn8_q81's
 planar Q8_1 output -- also against the float64 product of the dequantised
 weights and the float64 attention output as a sanity bound.
