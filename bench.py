@@ -47,20 +47,31 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def timed_events(fn, stream, n):
-    """Average ms per call of fn() over n back-to-back calls on `stream`,
-    bracketed by one pair of HIP events (launch overhead amortised, so the
-    figure tracks the kernel's own duration as rocprof reports it)."""
+def timed_reps(fn, stream, iters, reps=11):
+    """ms per call of fn() on `stream`, the way the reference's bench_attn.cu
+    times (tests/bench_attn.cu:125-142): `reps` repetitions, each one pair of
+    HIP events around `iters` back-to-back calls (launch overhead amortised, so
+    the figure tracks the kernel's own duration as rocprof reports it), the
+    average per call of each repetition, then the median over repetitions.
+    Returns {"median", "min", "max", "reps", "iters"} in ms."""
     import torch
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     fn()
     stream.synchronize()
-    a.record(stream)
-    for _ in range(n):
-        fn()
-    b.record(stream)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        for _ in range(iters):
+            fn()
+        b.record(stream)
     stream.synchronize()
-    return a.elapsed_time(b) / n
+    ms = sorted(a.elapsed_time(b) / iters for a, b in evs)
+    return {"median": ms[len(ms) // 2], "min": ms[0], "max": ms[-1], "reps": reps, "iters": iters}
+
+
+def spread_us(t):
+    """A timed_reps result in microseconds, for the results record."""
+    return {"median_us": t["median"] * 1e3, "min_us": t["min"] * 1e3, "max_us": t["max"] * 1e3,
+            "reps": t["reps"], "iters": t["iters"]}
 
 
 def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters):
@@ -76,15 +87,18 @@ def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters):
     for _ in range(warmup):
         graph.launch()
     st.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # one event between consecutive replays: the total over the K steps is the
+    # headline; the per-step spread is reported beside it
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     torch.cuda.synchronize()
-    e0.record(st)
-    for _ in range(steps):
+    evs[0].record(st)
+    for i in range(steps):
         graph.launch()
-    e1.record(st)
+        evs[i + 1].record(st)
     st.synchronize()
     torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / steps
+    ms_step = evs[0].elapsed_time(evs[-1]) / steps
+    per_step = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(steps))
     bytes_layer = seq * 2048.0
     us_layer = ms_step * 1e3 / layers
     gbs = bytes_layer * layers / (ms_step * 1e-3) / 1e9
@@ -97,14 +111,20 @@ def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters):
         lk.attn_split(qs[j], kcs[j], vcs[j], d_pos, part, stream=st)
 
     one_split()
-    split_ms = timed_events(one_split, st, kernel_iters)
-    comb_ms = timed_events(lambda: lk.attn_combine(part, d_pos, outs[0], None, stream=st), st, kernel_iters)
+    split_t = timed_reps(one_split, st, kernel_iters)
+    comb_t = timed_reps(lambda: lk.attn_combine(part, d_pos, outs[0], None, stream=st), st, kernel_iters)
     graph.close()
+    split_us, comb_us = split_t["median"] * 1e3, comb_t["median"] * 1e3
     res = {
         "seq": seq, "layers": layers, "ms_per_step": ms_step, "us_per_layer": us_layer,
-        "GBps": gbs, "split_us": split_ms * 1e3, "combine_us": comb_ms * 1e3,
-        "split_GBps": bytes_layer / (split_ms * 1e-3) / 1e9, "bytes_per_layer": bytes_layer,
-        "graph_nodes": 2 * layers,
+        "us_per_layer_step_spread": {"median": per_step[len(per_step) // 2] * 1e3 / layers,
+                                     "min": per_step[0] * 1e3 / layers, "max": per_step[-1] * 1e3 / layers},
+        "GBps": gbs, "layer_frac": gbs / HBM_PEAK_GBS,
+        "split_us": split_us, "combine_us": comb_us,
+        "split": spread_us(split_t), "combine": spread_us(comb_t),
+        "split_GBps": bytes_layer / (split_us * 1e-6) / 1e9,
+        "split_frac": bytes_layer / (split_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+        "bytes_per_layer": bytes_layer, "graph_nodes": 2 * layers,
     }
     del qs, kcs, vcs
     torch.cuda.empty_cache()
@@ -166,7 +186,7 @@ def pf_ops(m, P):
     return pairs * 64 * 2, pairs * 64 * 2, pairs
 
 
-def bench_prefill_c4(lk, lkc, iters):
+def bench_prefill_c4(lk, lkc, iters, reps=11):
     import torch
     qh, kc, vc, S = lkc.prefill_inputs("C4")
     m, P = S, 0
@@ -179,40 +199,56 @@ def bench_prefill_c4(lk, lkc, iters):
     ksc = torch.empty(8 * ks + 4, device="cuda")
     o = torch.empty(m, 2048, device="cuda")
     torch.cuda.synchronize()
-    q_ms = timed_events(lambda: lk.pf_q8(qh, m, None, q8, qsc, qcs, stream=st), st, iters)
-    k_ms = timed_events(lambda: lk.pf_k8(kc, 0, S, None, ks, k8, ksc, stream=st), st, iters)
+    q_t = timed_reps(lambda: lk.pf_q8(qh, m, None, q8, qsc, qcs, stream=st), st, iters)
+    k_t = timed_reps(lambda: lk.pf_k8(kc, 0, S, None, ks, k8, ksc, stream=st), st, iters)
     f8 = lambda: lk.pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
-    for _ in range(iters):                  # warm-up (clocks settle over the first ~100 us)
-        f8()
-    a8_ms = timed_events(f8, st, iters)
     f16 = lambda: lk.pf_attn(qh, m, P, kc, vc, o, stream=st)
-    for _ in range(iters):
-        f16()
-    a16_ms = timed_events(f16, st, iters)
     # the next GEMM's planar Q8_1: a separate pass over o, or fused (o not written)
     aqs = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
     asc = torch.empty(m, 64, 2, device="cuda")
     fq = lambda: (f8(), lk.pf_quant_rows(o, m, 2048, 64, aqs, asc, stream=st))
     ff = lambda: lk.pf_attn8_q81(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, None, aqs, asc, stream=st)
-    for f in (fq, ff):
-        for _ in range(iters):
-            f()
-    q_pass_ms = timed_events(fq, st, iters)
-    q_fused_ms = timed_events(ff, st, iters)
+    for _ in range(iters):                  # warm-up (clocks settle over the first ~100 us)
+        f8()
+    # int8 and fp16 kernels alternate repetition by repetition, so that a drift
+    # of the clocks during the run affects both alike
+    t8, t16 = [], []
+    for _ in range(reps):
+        t8.append(timed_reps(f8, st, iters, reps=1)["median"])
+        t16.append(timed_reps(f16, st, iters, reps=1)["median"])
+    t8.sort()
+    t16.sort()
+    a8_t = {"median": t8[reps // 2], "min": t8[0], "max": t8[-1], "reps": reps, "iters": iters}
+    a16_t = {"median": t16[reps // 2], "min": t16[0], "max": t16[-1], "reps": reps, "iters": iters}
+    q_pass_t = timed_reps(fq, st, iters, reps)
+    q_fused_t = timed_reps(ff, st, iters, reps)
+    a8_ms, a16_ms = a8_t["median"], a16_t["median"]
     oi, of, pairs = pf_ops(m, P)
     peak_ms = (oi / (PEAK_INT8_TOPS * 1e12) + of / (PEAK_FP16_TFLOPS * 1e12)) * 1e3
     return {
         "m": m, "P": P, "near": 1024, "sink": 1, "pairs": pairs,
         "attn8_us": a8_ms * 1e3, "attn8_TOPS": (oi + of) / (a8_ms * 1e-3) / 1e12,
-        "attn8_frac_of_mixed_peak": peak_ms / a8_ms,
+        "attn8_frac_of_mixed_peak": peak_ms / a8_ms, "attn8": spread_us(a8_t),
         "attn_fp16_us": a16_ms * 1e3, "attn_fp16_TOPS": (oi + of) / (a16_ms * 1e-3) / 1e12,
-        "q8_us": q_ms * 1e3, "k8_us": k_ms * 1e3,
-        "attn8_then_quant_rows_us": q_pass_ms * 1e3, "attn8_q81_fused_us": q_fused_ms * 1e3,
+        "attn_fp16_frac_of_mixed_peak": peak_ms / a16_ms, "attn_fp16": spread_us(a16_t),
+        "q8_us": q_t["median"] * 1e3, "k8_us": k_t["median"] * 1e3,
+        "attn8_then_quant_rows_us": q_pass_t["median"] * 1e3, "attn8_q81_fused_us": q_fused_t["median"] * 1e3,
+        "attn8_q81_fused": spread_us(q_fused_t),
     }
 
 
+C5_SAMPLE_CHUNKS = (65536, 126976)    # chunk starts whose sampled rows are checked
+C5_SAMPLE_ROWS = 6
+
+
 def bench_prefill_c5(lk, lkc, reps):
+    """C5: a 131072-token prompt in 32 chunks of 4096, the int8 kernel and the
+    fp16 kernel (every tile exact) alternating repetition by repetition; per
+    repetition the attention total over the 32 chunks (the quantisers are timed
+    apart).  Also returns the two kernels' outputs on sampled rows of two
+    chunks, which the CPU leg checks against float64 attention."""
     import torch
+    import numpy as np
     qh, kc, vc, S = lkc.prefill_inputs("C5")
     m = 4096
     ks = lk.kstride_for(S)
@@ -224,38 +260,59 @@ def bench_prefill_c5(lk, lkc, reps):
     ksc = torch.empty(8 * ks + 4, device="cuda")
     o = torch.empty(m, 2048, device="cuda")
     qchunks = [qh[p:p + m].contiguous() for p in range(0, S, m)]
+    rows = np.linspace(0, m - 1, C5_SAMPLE_ROWS).astype(np.int64)
+    samples = {}
     torch.cuda.synchronize()
-    best = None
-    for _ in range(reps):
+
+    def prompt(int8, keep):
         ev = []
         for c, P in enumerate(range(0, S, m)):
             a, b, c2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
             a.record(st)
-            lk.pf_k8(kc, P, P + m, None, ks, k8, ksc, stream=st)
-            lk.pf_q8(qchunks[c], m, None, q8, qsc, qcs, stream=st)
+            if int8:
+                lk.pf_k8(kc, P, P + m, None, ks, k8, ksc, stream=st)
+                lk.pf_q8(qchunks[c], m, None, q8, qsc, qcs, stream=st)
             b.record(st)
-            lk.pf_attn8(q8, qsc, qcs, qchunks[c], m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
+            if int8:
+                lk.pf_attn8(q8, qsc, qcs, qchunks[c], m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
+            else:
+                lk.pf_attn(qchunks[c], m, P, kc, vc, o, stream=st)
             c2.record(st)
             ev.append((a, b, c2))
+            if keep and P in C5_SAMPLE_CHUNKS:
+                st.synchronize()
+                samples.setdefault(P, {"rows": rows})["o8" if int8 else "o16"] = o[rows].cpu().numpy()
         st.synchronize()
-        quant = sum(a.elapsed_time(b) for a, b, _ in ev)
-        attn = sum(b.elapsed_time(c2) for _, b, c2 in ev)
-        if best is None or attn < best[1]:
-            best = (quant, attn)
+        return (sum(a.elapsed_time(b) for a, b, _ in ev), sum(b.elapsed_time(c2) for _, b, c2 in ev))
+
+    prompt(True, True)                                  # warm-up, and the sampled outputs
+    prompt(False, True)
+    t8, t16, tq = [], [], []
+    for _ in range(reps):
+        q_ms, a_ms = prompt(True, False)
+        tq.append(q_ms)
+        t8.append(a_ms)
+        t16.append(prompt(False, False)[1])
+    t8.sort(); t16.sort(); tq.sort()
     oi = of = 0.0
     for P in range(0, S, m):
         a, b, _ = pf_ops(m, P)
         oi += a
         of += b
-    quant_ms, attn_ms = best
     peak_ms = (oi / (PEAK_INT8_TOPS * 1e12) + of / (PEAK_FP16_TFLOPS * 1e12)) * 1e3
+    attn_ms, a16_ms = t8[len(t8) // 2], t16[len(t16) // 2]
     del qh, kc, vc, qchunks, k8
     torch.cuda.empty_cache()
     return {
-        "chunks": S // m, "chunk": m, "attn_ms": attn_ms, "quant_ms": quant_ms,
+        "chunks": S // m, "chunk": m, "reps": reps,
+        "attn_ms": attn_ms, "attn_ms_min": t8[0], "attn_ms_max": t8[-1],
+        "quant_ms": tq[len(tq) // 2],
         "attn8_TOPS": (oi + of) / (attn_ms * 1e-3) / 1e12,
         "attn8_frac_of_mixed_peak": peak_ms / attn_ms,
-    }
+        "attn_fp16_ms": a16_ms, "attn_fp16_ms_min": t16[0], "attn_fp16_ms_max": t16[-1],
+        "attn_fp16_TOPS": (oi + of) / (a16_ms * 1e-3) / 1e12,
+        "attn_fp16_frac_of_mixed_peak": peak_ms / a16_ms,
+    }, samples
 
 
 def bench_read_reference(lk, bytes_list=(67108864, 268435456), nbuf=10, iters=20):
@@ -305,15 +362,17 @@ def bench_gemv(lk, nmat=128, iters=256):
     for i in range(nmat):
         f(i)
     st.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for i in range(iters):
-        f(i)
-    e1.record(st); e1.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / iters
+    ctr = [0]
+
+    def one():
+        f(ctr[0])
+        ctr[0] += 1
+
+    t = timed_reps(one, st, iters)
+    us = t["median"] * 1e3
     nbytes = rows * bpr * 18 + bpr * 36 + rows * 8
     return {"rows": rows, "bpr": bpr, "us": us, "GBps": nbytes / (us * 1e-6) / 1e9, "bytes": nbytes,
-            "distinct_weight_matrices": nmat}
+            "distinct_weight_matrices": nmat, "spread": spread_us(t)}
 
 
 def bench_pf_gemm(lk, ntok=4096, N=2048, bpr=64, iters=20):
@@ -332,10 +391,11 @@ def bench_pf_gemm(lk, ntok=4096, N=2048, bpr=64, iters=20):
     f = lambda: lk.pf_gemm_q4_0(qs, d, N, bpr, aqs, asc, ntok, out, N, True, stream=st)
     for _ in range(iters):
         f()
-    ms = timed_events(f, st, iters)
+    t = timed_reps(f, st, iters)
+    ms = t["median"]
     ops = 2.0 * N * 32 * bpr * ntok
     return {"ntok": ntok, "N": N, "K": 32 * bpr, "us": ms * 1e3, "TOPS": ops / (ms * 1e-3) / 1e12,
-            "frac_of_int8_peak": ops / (ms * 1e-3) / (PEAK_INT8_TOPS * 1e12)}
+            "frac_of_int8_peak": ops / (ms * 1e-3) / (PEAK_INT8_TOPS * 1e12), "spread": spread_us(t)}
 
 
 def bench_producers(lk, iters):
@@ -367,9 +427,9 @@ def bench_producers(lk, iters):
     for f in (f0, f1, f2):
         for _ in range(iters):
             f()
-    t0 = timed_events(f0, st, iters)
-    t1 = timed_events(f1, st, iters)
-    t2 = timed_events(f2, st, iters)
+    t0 = timed_reps(f0, st, iters)["median"]
+    t1 = timed_reps(f1, st, iters)["median"]
+    t2 = timed_reps(f2, st, iters)["median"]
     b0 = m * 3072 * 4 + m * 2048 * 2 + m * 512 * 2 * 2
     b1 = b0 + m * 512 + m * 8 * 4
     qf = torch.randn(2048, device="cuda", generator=g)
@@ -379,7 +439,7 @@ def bench_producers(lk, iters):
     fd = lambda: lk.qk_norm_rope(qf, kf, vf, qn, kn, d_pos, kc, vc, stream=st)
     for _ in range(iters):
         fd()
-    td = timed_events(fd, st, iters)
+    td = timed_reps(fd, st, iters)["median"]
     return {
         "m": m, "qknr_us": t0 * 1e3, "qknr_GBps": b0 / (t0 * 1e-3) / 1e9, "qknr_bytes": b0,
         "qknr_k8_fused_us": t1 * 1e3, "qknr_k8_fused_GBps": b1 / (t1 * 1e-3) / 1e9,
@@ -426,12 +486,18 @@ def bench_pf_driver(lk, n_tok=32768, chunks=(4096, 8192)):
     return {"prompt_tokens": n_tok, "layers": 1, **res}
 
 
-def cpu_baseline(seconds, prefill=True):
+def cpu_baseline(seconds, prefill=True, c5_samples=None):
     """The reference's CPU path restated in the oracle (float64, single
     thread): decode attention (tests/test_attn.cu:46-74) on a full C2 layer and
     on C1, and prefill attention (tests/test_prefill.cu:263-282) on sampled
     query rows of C4 and of C5's last chunk, extrapolated by the number of
-    (query, key) pairs to the whole chunk / prompt."""
+    (query, key) pairs to the whole chunk / prompt.
+
+    With c5_samples (the GPU kernels' outputs on sampled rows of C5 chunks),
+    the float64 attention of those rows is also the checker of the int8 and
+    fp16 kernels' accuracy, the figure the reference reports for its int8
+    scoring (tests/test_prefill.cu:862-866, src/engine.cu:245-248): rel-RMS =
+    RMS(err) / RMS(ref) and max-rel = max|err| / max|ref| over the rows."""
     import numpy as np
     import torch
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -460,7 +526,6 @@ def cpu_baseline(seconds, prefill=True):
         P = 0 if cfg == "C4" else S - m
         rows = np.linspace(0, m - 1, nrows).astype(np.int32)
         Q, K, V = h16(qh[P:P + m]), h16(kc[:P + m]), h16(vc[:P + m])
-        del qh, kc, vc
         t0 = time.perf_counter()
         orc.pf_ref(Q, m, P, K, V, rows=rows)
         dt = time.perf_counter() - t0
@@ -475,6 +540,20 @@ def cpu_baseline(seconds, prefill=True):
                     "sample_s": dt, "sample_pairs": pairs_s,
                     "note": "float64 reference on sampled query rows (all 32 heads), "
                             "extrapolated by (query, key) pairs"}
+        if cfg == "C5" and c5_samples:
+            acc = {}
+            for P0, smp in sorted(c5_samples.items()):
+                r = np.asarray(smp["rows"], np.int32)
+                ref = orc.pf_ref(h16(qh[P0:P0 + m]), m, P0, h16(kc[:P0 + m]), h16(vc[:P0 + m]), rows=r)[r]
+                ent = {"rows": [int(x) for x in r]}
+                for key, name in (("o8", "int8"), ("o16", "fp16")):
+                    if key in smp:
+                        e = smp[key].astype(np.float64) - ref
+                        ent[name] = {"rel_rms": float(np.sqrt(np.mean(e * e)) / np.sqrt(np.mean(ref * ref))),
+                                     "max_rel": float(np.max(np.abs(e)) / np.max(np.abs(ref)))}
+                acc[f"P{P0}"] = ent
+            res["C5_accuracy"] = acc
+        del qh, kc, vc
         torch.cuda.empty_cache()
     return res
 
@@ -586,12 +665,13 @@ def main():
     log("decode step graph with the attention output projection (3 nodes per layer)")
     results["C2_decode_step_graph_wo"] = bench_decode_step(lk, 50, 10, with_wo=True)
     log(json.dumps(results["C2_decode_step_graph_wo"]))
+    c5_samples = None
     if not args.skip_prefill:
         log("prefill C4 (4096 chunk, P=0)")
         results["C4_prefill_4k"] = bench_prefill_c4(lk, lkc, 20)
         log(json.dumps(results["C4_prefill_4k"]))
         log("prefill C5 (131072 prompt, 32 chunks)")
-        results["C5_prefill_131k"] = bench_prefill_c5(lk, lkc, 2)
+        results["C5_prefill_131k"], c5_samples = bench_prefill_c5(lk, lkc, 3)
         log(json.dumps(results["C5_prefill_131k"]))
         log("prefill attention-output GEMM (4096 tokens x 2048 x 2048 Q4_0)")
         results["pf_attn_out_gemm"] = bench_pf_gemm(lk)
@@ -606,7 +686,9 @@ def main():
     cpu = None
     if not args.skip_cpu:
         log("cpu baseline (float64 oracle, 1 thread)")
-        cb = cpu_baseline(args.cpu_seconds, prefill=not args.skip_prefill)
+        cb = cpu_baseline(args.cpu_seconds, prefill=not args.skip_prefill, c5_samples=c5_samples)
+        if "C5_accuracy" in cb:
+            results["C5_prefill_131k"]["accuracy_vs_float64"] = cb.pop("C5_accuracy")
         results["cpu_float64"] = cb
         cpu = {"value": cb["C2"]["GBps"], "unit": "GB/s", "cores": 1, "kind": "port",
                "sample": f"full C2 layer (32q/8kv/64, ctx 32768) float64 decode attention, "
