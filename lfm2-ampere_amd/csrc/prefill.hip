@@ -219,13 +219,6 @@ struct PfWork {
 // Static scratch for the partials, 64 MiB per device.
 #define PF_PART_CAP   (16u << 20)                        // floats
 __device__ float g_pf_part[PF_PART_CAP];
-#ifdef PF_WG_TRACE
-// Measurement builds only: per-workgroup (start, end, HW_ID, XCC_ID).
-__device__ uint4 g_pf_trace[16384];
-extern "C" int lk_pf_trace_read(void * dst, int n) {
-    return (int) hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_pf_trace), (size_t) n * sizeof(uint4));
-}
-#endif
 
 // ---- planar Q8_1 of the attention output (the next GEMM's input) -------------
 // Reference k_pf_quant_rows / pf_quant_warp (prefill.cu:1574-1580, 90-103): per
@@ -289,20 +282,6 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     __shared__ PfStage st[2];
     __shared__ __attribute__((aligned(16))) int8_t s_q[4][PF_BQ * PF_Q_LD];   // fp16 Q, per head
     __shared__ __attribute__((aligned(16))) float s_kp[4][2 * PF_BK];          // per wave: ks', -PF_MAGIC*ks'
-#ifdef PF_WG_TRACE
-    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
-    auto trace_end = [&](int ntiles) {
-        if (threadIdx.x == 0) {
-            const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
-            const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
-            const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);
-            const unsigned id = blockIdx.x + blockIdx.y * gridDim.x;
-            if (id < 8192) g_pf_trace[id] = make_uint4((unsigned) t_start, (unsigned) t_end, hw, (xcc & 255) | ((unsigned) ntiles << 8));
-        }
-    };
-#else
-    auto trace_end = [](int) {};
-#endif
     // Causal work grows with the query block.  Unsplit launches: workgroups
     // are dispatched in linear order and the second half of the grid lands
     // beside the first half on the CUs, so kv heads 0-3 take the query blocks
@@ -323,9 +302,6 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         kt_lo = (int) (kr & 0xffff);
         kt_hi = (int) (kr >> 16);
     }
-#ifdef PF_WG_TRACE
-    const uint64_t t_w = __builtin_amdgcn_s_memrealtime();
-#endif
     const int tid  = threadIdx.x;
     const int lane = tid & 63;
     const int w    = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -460,9 +436,6 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         }
     }
 
-#ifdef PF_WG_TRACE
-    const uint64_t t_q = __builtin_amdgcn_s_memrealtime();
-#endif
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
     // all-ones A operand, so every lane of query column q accumulates
     // l_q = sum of the same fp16 P the numerator uses.
@@ -674,24 +647,12 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     };
 
     // ---- tile loop: one barrier per tile; tile kt+1 streams in while kt computes
-#ifdef PF_WG_TRACE
-    uint64_t t_a = __builtin_amdgcn_s_memrealtime(), t_b = 0, t_c = 0;
-#endif
     for (int kt = kt_lo; kt < kt_hi; ++kt) {
         lk_wait_vm<0>();                                  // this wave's part of tile kt landed
         __syncthreads();                                  // ... everyone's; tile kt-1 fully consumed
-#ifdef PF_WG_TRACE
-        if (kt == kt_lo) t_b = __builtin_amdgcn_s_memrealtime();
-        if (kt == kt_lo + 1) t_c = __builtin_amdgcn_s_memrealtime();
-#endif
         if (kt + 1 < kt_hi) issue(kt + 1);                // into the stage tile kt-1 used
         tile(st[kt & 1], kt);
     }
-#ifdef PF_WG_TRACE
-    if (threadIdx.x == 0 && blockIdx.x + blockIdx.y * gridDim.x < 8192)
-        g_pf_trace[8192 + blockIdx.x + blockIdx.y * gridDim.x] = make_uint4((unsigned) t_a, (unsigned) t_b, (unsigned) t_c,
-                                                                        (unsigned) ((t_w - t_start) & 0xffff) | ((unsigned) ((t_q - t_start) & 0xffff) << 16));
-#endif
 
     if (pslot >= 0) {                                     // a part: unnormalised partial
         float * R = pbuf + (size_t) (pslot * LK_N_KV_HEADS + kvh) * PF_PART_SLOT;
@@ -704,7 +665,6 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             for (int db = 0; db < 4; ++db) A[(4 * db + g) * PF_BQ + row] = acc[db][qb];
             if (g == 0) ML[row] = make_float2(fmaf(mrun[qb], sq[qb], PF_P_BIAS), acc[4][qb][0]);
         }
-        trace_end(kt_hi - kt_lo);
         return;
     }
 
@@ -725,7 +685,6 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         if (aqs) lk_pf_q81_epilogue(a, qr < m, aqs + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM,
                                     asc + (size_t) qr * (LK_HIDDEN / 32) + 2 * head, g);
     }
-    trace_end(kt_hi - kt_lo);
 }
 
 // Merge of the parts of split query blocks: workgroup (split block, kv head,
