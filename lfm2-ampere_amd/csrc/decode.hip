@@ -358,16 +358,11 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
 
 // Q8_1 quantisation of the 64 outputs of one head held by one wave, one value
 // per lane, two 32-lane blocks (reference quant.cuh:106-121): exact max, a
-// fixed xor butterfly 16,8,4,2,1 for the raw sum, d = amax/127 (IEEE
+// fixed xor butterfly 16,8,4,2,1 for the raw sum (lk_bfly32_sum), d = amax/127 (IEEE
 // division), q = roundf(x/d), (d, sum) stored as fp16 RNE.
 __device__ __forceinline__ void lk_quant_q8_1_wave(float x, lk_block_q8_1 * __restrict__ yq8) {
     const int lane = threadIdx.x & 63;
-    float am = fabsf(x), sum = x;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-        am = fmaxf(am, __shfl_xor(am, o, 32));
-        sum += __shfl_xor(sum, o, 32);
-    }
+    const float am = lk_bfly32_max(fabsf(x)), sum = lk_bfly32_sum(x);
     const float d = am / 127.0f;
     const int8_t qv = (am == 0.0f) ? (int8_t) 0 : (int8_t) roundf(x / d);
     lk_block_q8_1 * b = yq8 + (lane >> 5);
@@ -383,12 +378,7 @@ __device__ __forceinline__ void lk_quant_q8_1_wave(float x, lk_block_q8_1 * __re
 // (lanes 32..63 hold a copy and write nothing).
 __device__ __forceinline__ void lk_quant_q8_1_half(float x, lk_block_q8_1 * __restrict__ b) {
     const int lane = threadIdx.x & 63;
-    float am = fabsf(x), sum = x;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-        am = fmaxf(am, __shfl_xor(am, o, 32));
-        sum += __shfl_xor(sum, o, 32);
-    }
+    const float am = lk_bfly32_max(fabsf(x)), sum = lk_bfly32_sum(x);
     const float d = am / 127.0f;
     const int8_t qv = (am == 0.0f) ? (int8_t) 0 : (int8_t) roundf(x / d);
     if (lane < 32) b->qs[lane] = qv;

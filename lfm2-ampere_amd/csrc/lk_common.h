@@ -112,6 +112,44 @@ __device__ __forceinline__ float lk_xrow_sum(float x) {
 __device__ __forceinline__ float lk_xrow_sum(float x) { return x; }
 #endif
 
+// The xor butterfly over the 32 lanes of each half-wave with offsets 16, 8,
+// 4, 2, 1 (the order of __shfl_xor loops of width 32), on lane swaps and DPP
+// instead of LDS permutes: offset 16 is v_permlane16_swap, 8 is row_ror:8
+// (lane i of a 16-lane row meets i+8 mod 16 = i^8), 4 is row_ror:4 (lane i
+// meets i+4 mod 16, which after the offset-8 step holds the same value as
+// i^4), 2 and 1 are quad permutes.  Every step adds (or maxes) the same two
+// operands in both partner lanes, so all 32 lanes end with identical bits,
+// equal to the __shfl_xor butterfly's.
+#define LK_DPP_ROR8      0x128
+#define LK_DPP_ROR4      0x124
+#ifdef __HIP_DEVICE_COMPILE__
+__device__ __forceinline__ void lk_swap16(float & a, float & b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+#else
+__device__ __forceinline__ void lk_swap16(float &, float &) {}
+#endif
+__device__ __forceinline__ float lk_bfly32_sum(float x) {
+    float a = x, b = x;
+    lk_swap16(a, b);
+    float v = a + b;
+    v += lk_dpp<LK_DPP_ROR8>(v);
+    v += lk_dpp<LK_DPP_ROR4>(v);
+    v += lk_dpp<LK_DPP_QP_XOR2>(v);
+    v += lk_dpp<LK_DPP_QP_XOR1>(v);
+    return v;
+}
+__device__ __forceinline__ float lk_bfly32_max(float x) {
+    float a = x, b = x;
+    lk_swap16(a, b);
+    float v = fmaxf(a, b);
+    v = fmaxf(v, lk_dpp<LK_DPP_ROR8>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_ROR4>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR2>(v));
+    v = fmaxf(v, lk_dpp<LK_DPP_QP_XOR1>(v));
+    return v;
+}
+
 // Four fp16 of one column from a row-major LDS tile via the gfx950 transpose
 // read (ds_read_b64_tr_b16).  Within each 16-lane group, lane 4a+b supplies
 // the address of T[row0 + a][col0 + 4b .. +3]; lane c then receives

@@ -791,12 +791,7 @@ lk_k_pf_quant_rows(const float * __restrict__ X, int ld, int kb, int8_t * __rest
     const int b = blockIdx.y * 8 + (threadIdx.x >> 5), lane = threadIdx.x & 31;
     const bool ok = b < kb;                               // half-wave uniform
     const float x = ok ? X[(size_t) r * ld + b * 32 + lane] : 0.0f;
-    float am = fabsf(x), sum = x;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) {
-        am = fmaxf(am, __shfl_xor(am, o, 32));
-        sum += __shfl_xor(sum, o, 32);
-    }
+    const float am = lk_bfly32_max(fabsf(x)), sum = lk_bfly32_sum(x);
     const float d = am / 127.0f;
     if (!ok) return;
     qs[(size_t) r * kb * 32 + b * 32 + lane] = lk_q81_q(x, am, d);
