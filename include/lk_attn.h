@@ -240,6 +240,16 @@ int lk_pf_quant_rows(const float * X, int rows, int ld, int kb, int8_t * qs, flo
  * split). */
 int lk_pf_split_override(int tiles);
 
+/* Paired launches: one 8-wave workgroup per (kv head, block pair i, nq-1-i) of
+ * a chunk, the two 4-wave halves sharing the key tiles block i sees, then
+ * splitting the rest of block nq-1-i between them (merged in LDS, fixed order).
+ * Every workgroup does the same work, so a 4096-row chunk at P = 0 needs no
+ * split.  Process-wide knob, for tests and tuning: -1 never, 0 automatic
+ * (default: the fp16 kernel on chunks of at least 64 blocks with P <= m), 1
+ * whenever the chunk has two or more blocks (both kernels).  No counterpart in
+ * the reference. */
+int lk_pf_pair_override(int mode);
+
 /* ---- attention-input producers ---------------------------------------------
  * Per-head RMS norm (eps 1e-5) of q and k with weights qn / kn (fp32 [64]),
  * NEOX rotary embedding (theta 1e7) at the token's position, and the fp16

@@ -271,25 +271,55 @@ __device__ __forceinline__ void lk_pf_q81_epilogue(const lk_f4 (&a)[4], bool sto
     }
 }
 
-template <bool INT8>
-__global__ void __launch_bounds__(256, 2)
+// PAIR: workgroups of 8 waves, each over query blocks bi = pair index and
+// bj = nq-1-bi of one kv head.  Waves 0-3 (group A) and 4-7 (group B) share
+// one key-tile stream: while both blocks see the tile (keys of block bi's
+// range) group A scores it for bi and group B for bj; the rest of bj's tiles
+// alternate between the groups, two tiles per step, and at the end group A's
+// part of bj is merged into group B's through LDS.  Every workgroup then
+// does the same work (about half of bi + bj), with no split-K partials in
+// memory and no merge kernel.
+template <bool INT8, bool PAIR>
+__global__ void __launch_bounds__(PAIR ? 512 : 256, PAIR ? 1 : 2)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
              const float * __restrict__ qcs, const _Float16 * __restrict__ qh, int m, int P,
              const int8_t * __restrict__ k8, const float * __restrict__ ksc, int kstride,
              const _Float16 * __restrict__ kc, const _Float16 * __restrict__ vc,
              int near, int sink, float * __restrict__ o, int8_t * __restrict__ aqs,
              float2 * __restrict__ asc, const PfWork work, float * __restrict__ pbuf) {
-    __shared__ PfStage st[2];
-    __shared__ __attribute__((aligned(16))) int8_t s_q[4][PF_BQ * PF_Q_LD];   // fp16 Q, per head
-    __shared__ __attribute__((aligned(16))) float s_kp[4][2 * PF_BK];          // per wave: ks', -PF_MAGIC*ks'
+    constexpr int NW = PAIR ? 8 : 4;                     // waves
+    __shared__ PfStage st[PAIR ? 4 : 2];                  // PAIR: [stage][slot]
+    __shared__ __attribute__((aligned(16))) int8_t s_q[NW][PF_BQ * PF_Q_LD];  // fp16 Q, per wave
+    __shared__ __attribute__((aligned(16))) float s_kp[NW][2 * PF_BK];         // per wave: ks', -PF_MAGIC*ks'
     // Causal work grows with the query block.  Unsplit launches: workgroups
     // are dispatched in linear order and the second half of the grid lands
     // beside the first half on the CUs, so kv heads 0-3 take the query blocks
     // longest-first and kv heads 4-7 shortest-first: co-resident workgroups
     // then pair a long block with a short one.  Split launches: one work item
     // (block, key range) per workgroup, longest first.
+    const int tid  = threadIdx.x;
+    const int lane = tid & 63;
+    const int w    = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col  = lane & 15, g = lane >> 4;
+    const int hw   = w & 3, grp = w >> 2;                 // head within the kv head; PAIR group
     int kvh, qt, kt_lo, kt_hi, pslot = -1;
-    if (work.n_items == 0) {
+    int bi = 0, bj = 0, nki = 0, nkj = 0;                 // PAIR: the two blocks, their tile counts
+    bool a2 = true;                                       // PAIR: group A takes half of bj's later tiles
+    if constexpr (PAIR) {
+        kvh = blockIdx.x % LK_N_KV_HEADS;
+        const int nq = (m + PF_BQ - 1) / PF_BQ;
+        bi = (int) (blockIdx.x / LK_N_KV_HEADS);
+        bj = nq - 1 - bi;
+        nki = (bi == bj) ? 0 : pf_nkt(bi, m, P);
+        nkj = pf_nkt(bj, m, P);
+        // Group A's first tile of bj (tile nki) must hold a key that every row
+        // of bj sees, or a row would start A's part with no visible key; only
+        // bj = bi+1 with P not a multiple of 64 breaks that, and then group B
+        // takes all of bj's remaining tiles.
+        a2 = nki == 0 || nki * PF_BK <= P + bj * PF_BQ;
+        qt = (grp == 0 && nki > 0) ? bi : bj;             // group A starts on bi when it has one
+        kt_lo = 0; kt_hi = 0;
+    } else if (work.n_items == 0) {
         kvh = blockIdx.y;
         qt  = (kvh < LK_N_KV_HEADS / 2) ? (int) (gridDim.x - 1 - blockIdx.x) : (int) blockIdx.x;
         kt_lo = 0; kt_hi = pf_nkt(qt, m, P);
@@ -302,58 +332,71 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         kt_lo = (int) (kr & 0xffff);
         kt_hi = (int) (kr >> 16);
     }
-    const int tid  = threadIdx.x;
-    const int lane = tid & 63;
-    const int w    = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int col  = lane & 15, g = lane >> 4;
-    const int head = kvh * LK_G + w;
-    const int qbase = qt * PF_BQ;
-    const int qlast = (qbase + PF_BQ < m) ? (qbase + PF_BQ) : m;
-    const int kend = P + qlast;                       // keys [0, kend) are visible to some row
-    const int qt32_lo = qbase / 32, qt32_hi = qbase / 32 + 1;
+    const int head = kvh * LK_G + hw;
+    int qbase = qt * PF_BQ;                           // the wave's block (PAIR group A moves to bj)
+    // keys [0, kend) are visible to some row of the workgroup's blocks (PAIR: of bj)
+    const int kend = P + (PAIR ? (bj * PF_BQ + PF_BQ < m ? bj * PF_BQ + PF_BQ : m)
+                               : (qbase + PF_BQ < m ? qbase + PF_BQ : m));
 
-    auto mode_of = [&](int kt) -> int {
+    // tile mode for the 64-query block starting at query qb0
+    auto mode_at = [&](int kt, int qb0) -> int {
         if (!INT8) return PF_EXACT;
-        if (lk_pf_exact(P, qt32_hi, kt, near, sink)) return PF_EXACT;
-        return lk_pf_exact(P, qt32_lo, kt, near, sink) ? PF_MIXED : PF_INT8;
+        if (lk_pf_exact(P, qb0 / 32 + 1, kt, near, sink)) return PF_EXACT;
+        return lk_pf_exact(P, qb0 / 32, kt, near, sink) ? PF_MIXED : PF_INT8;
     };
+    auto mode_of = [&](int kt) -> int { return mode_at(kt, qbase); };
     // a tile needs the causal mask iff its last key lies past the first query
     auto mask_of = [&](int kt) -> bool { return kt * PF_BK + PF_BK - 1 > P + qbase; };
 
-    // ---- LDS DMA of tile kt: wave w fetches keys 16w .. 16w+15 ----------------
+    // ---- LDS DMA of tile kt: wave hw (of the issuing four) fetches keys 16hw .. 16hw+15
     const uint32_t lds_st = lk_lds_addr(&st[0]);
     const float * ks_h = INT8 ? ksc + (size_t) kvh * kstride : nullptr;
     const int ks_clamp = ((kend - 1) / 4) * 4;        // last 16-byte chunk holding a visible key
     // Per-lane byte offsets of the DMA sources relative to the tile's first key
     // (the kv head folded in); the tile base itself is wave-uniform.
-    const int r_k8 = 16 * w + (lane >> 2);
-    const uint32_t so_k8 = (uint32_t) ((r_k8 * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 16 * ((lane & 3) ^ pf_sw_k8(r_k8)));
-    const uint32_t so_ks = (uint32_t) (4 * (16 * w + 4 * lane));
-    uint32_t so_kh[2], so_v[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int r = 16 * w + 8 * j + (lane >> 3);
+    // PAIR: the offsets are recomputed at each issue from an opaque copy of
+    // the lane id (the compiler would otherwise keep five of them live across
+    // the loop, at a register budget that leaves no room for them).
+    auto dma_lane = [&]() -> int {
+        if constexpr (PAIR) {
+            int l;
+            asm volatile("v_mov_b32 %0, %1" : "=v"(l) : "v"(lane));
+            return l;
+        } else {
+            return lane;
+        }
+    };
+    auto so_k8_of = [&](int ln) -> uint32_t {
+        const int r = 16 * hw + (ln >> 2);
+        return (uint32_t) ((r * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM + 16 * ((ln & 3) ^ pf_sw_k8(r)));
+    };
+    auto so_ks_of = [&](int ln) -> uint32_t { return (uint32_t) (4 * (16 * hw + 4 * ln)); };
+    auto so_kv_of = [&](int ln, int j, bool isv) -> uint32_t {
+        const int r = 16 * hw + 8 * j + (ln >> 3);
         const uint32_t row = (uint32_t) ((r * LK_N_KV_HEADS + kvh) * LK_HEAD_DIM * 2);
-        so_kh[j] = row + 16 * ((lane & 7) ^ pf_sw_kh(r));
-        so_v[j]  = row + 16 * ((lane & 7) ^ pf_sw_v(r));
-    }
-    auto issue = [&](int kt) {
-        const int md = mode_of(kt);
-        const uint32_t sb = lds_st + (uint32_t) ((kt & 1) * sizeof(PfStage));
+        return row + 16 * ((ln & 7) ^ (isv ? pf_sw_v(r) : pf_sw_kh(r)));
+    };
+    // into stage buffer si; md = the union of the readers' tile modes
+    auto issue_to = [&](int kt, int si, int md) {
+        const uint32_t sb = lds_st + (uint32_t) (si * sizeof(PfStage));
         const int kb0 = kt * PF_BK;
+        const int ln = dma_lane();
+        const uint32_t so_k8 = so_k8_of(ln), so_ks = so_ks_of(ln);
+        const uint32_t so_kh[2] = {so_kv_of(ln, 0, false), so_kv_of(ln, 1, false)};
+        const uint32_t so_v[2] = {so_kv_of(ln, 0, true), so_kv_of(ln, 1, true)};
         if (kb0 + PF_BK <= kend) {                        // whole tile visible: no clamping
             const int8_t * kb8 = k8 + (size_t) kb0 * LK_KV_ROW;
             const _Float16 * kbh = kc + (size_t) kb0 * LK_KV_ROW;
             const _Float16 * kbv = vc + (size_t) kb0 * LK_KV_ROW;
             if (md != PF_EXACT) {
-                lk_dma16c_so(kb8, so_k8, sb + (uint32_t) (offsetof(PfStage, k8) + 1024 * w));
-                if (lane < 4) lk_dma16c_so(ks_h + kb0, so_ks, sb + (uint32_t) (offsetof(PfStage, ks) + 64 * w));
+                lk_dma16c_so(kb8, so_k8, sb + (uint32_t) (offsetof(PfStage, k8) + 1024 * hw));
+                if (lane < 4) lk_dma16c_so(ks_h + kb0, so_ks, sb + (uint32_t) (offsetof(PfStage, ks) + 64 * hw));
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 if (md != PF_INT8)
-                    lk_dma16c_so(kbh, so_kh[j], sb + (uint32_t) (offsetof(PfStage, kh) + 1024 * (2 * w + j)));
-                lk_dma16c_so(kbv, so_v[j], sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * w + j)));
+                    lk_dma16c_so(kbh, so_kh[j], sb + (uint32_t) (offsetof(PfStage, kh) + 1024 * (2 * hw + j)));
+                lk_dma16c_so(kbv, so_v[j], sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * hw + j)));
             }
             return;
         }
@@ -365,76 +408,105 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         const _Float16 * kbh = kc + (size_t) kb0 * LK_KV_ROW;
         const _Float16 * kbv = vc + (size_t) kb0 * LK_KV_ROW;
         if (md != PF_EXACT) {
+            const int r_k8 = 16 * hw + (ln >> 2);
             const int rr = (r_k8 < lim) ? r_k8 : lim;
             lk_dma16c_so(kb8, so_k8 + (uint32_t) ((rr - r_k8) * LK_KV_ROW),
-                         sb + (uint32_t) (offsetof(PfStage, k8) + 1024 * w));
+                         sb + (uint32_t) (offsetof(PfStage, k8) + 1024 * hw));
             if (lane < 4) {
-                const int s0 = 16 * w + 4 * lane, sl = ks_clamp - kb0;
+                const int s0 = 16 * hw + 4 * ln, sl = ks_clamp - kb0;
                 lk_dma16c_so(ks_h + kb0, (uint32_t) (4 * (s0 < sl ? s0 : sl)),
-                             sb + (uint32_t) (offsetof(PfStage, ks) + 64 * w));
+                             sb + (uint32_t) (offsetof(PfStage, ks) + 64 * hw));
             }
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int r = 16 * w + 8 * j + (lane >> 3);
+            const int r = 16 * hw + 8 * j + (ln >> 3);
             const uint32_t dr = (uint32_t) ((((r < lim) ? r : lim) - r) * LK_KV_ROW * 2);
             if (md != PF_INT8)
-                lk_dma16c_so(kbh, so_kh[j] + dr, sb + (uint32_t) (offsetof(PfStage, kh) + 1024 * (2 * w + j)));
-            lk_dma16c_so(kbv, so_v[j] + dr, sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * w + j)));
+                lk_dma16c_so(kbh, so_kh[j] + dr, sb + (uint32_t) (offsetof(PfStage, kh) + 1024 * (2 * hw + j)));
+            lk_dma16c_so(kbv, so_v[j] + dr, sb + (uint32_t) (offsetof(PfStage, v) + 1024 * (2 * hw + j)));
+        }
+    };
+
+    auto issue = [&](int kt) { issue_to(kt, kt & 1, mode_of(kt)); };
+    // PAIR: the tiles of step it (one tile both groups read, then two tiles,
+    // one per group, into the step's two slots); waves 0-3 fetch slot 0,
+    // waves 4-7 slot 1
+    auto issue_step = [&](int it) {
+        const int si = 2 * (it & 1);
+        if (it < nki) {
+            if (grp == 0) {
+                const int ma = mode_at(it, bi * PF_BQ);
+                const int mb = mode_at(it, bj * PF_BQ);
+                const bool n8 = ma != PF_EXACT || mb != PF_EXACT, n16 = ma != PF_INT8 || mb != PF_INT8;
+                issue_to(it, si, n8 ? (n16 ? PF_MIXED : PF_INT8) : PF_EXACT);
+            }
+        } else if (a2) {
+            const int kt = nki + 2 * (it - nki) + grp;
+            if (kt < nkj) issue_to(kt, si + grp, mode_at(kt, bj * PF_BQ));
+        } else if (grp == 1) {
+            issue_to(it, si + 1, mode_at(it, bj * PF_BQ));
         }
     };
 
     // The first tile's DMA goes out before the Q loads below, so that the two
     // memory latencies overlap.
-    issue(kt_lo);
+    if constexpr (PAIR) issue_step(0);
+    else issue(kt_lo);
 
     // ---- this wave's fp16 Q block (64 rows x 128 B), for exact tiles, and the
     // int8 Q operands and scales below.  Every load reads a row clamped to m-1
     // and rows past m are zeroed by a select afterwards (a guarded load costs a
     // branch and a full memory wait each), and all of them are issued before
     // the first use: one memory round trip for the whole prologue.
-    lk_h8 qv16[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int qr = qbase + (lane >> 3) + 8 * i;
-        qv16[i] = *(const lk_h8 *) (qh + (size_t) (qr < m ? qr : m - 1) * LK_HIDDEN + head * LK_HEAD_DIM + 8 * (lane & 7));
-    }
-    // ---- int8 Q operands and per-query scalars (lane column = query) ----------
     lk_i4 qf8[PF_QB];
     float sq[PF_QB], exa[PF_QB], exb[PF_QB];   // exa, exb: see below
+    auto load_q = [&](bool fill_s_q) {
+        lk_h8 qv16[8];
+        if (fill_s_q) {
 #pragma unroll
-    for (int qb = 0; qb < PF_QB; ++qb) {
-        const int qr = qbase + 16 * qb + col;
-        const bool ok = qr < m;
-        const int qrc = ok ? qr : m - 1;                  // clamped: unconditional loads
-        const lk_i4 zi = { 0, 0, 0, 0 };
-        if (INT8) {
-            const lk_i4 qv = *(const lk_i4 *) (q8 + (size_t) qrc * LK_HIDDEN + head * LK_HEAD_DIM + 16 * g);
-            const float dv = qsc[(size_t) qrc * LK_N_HEADS + head];
-            const float cv = qcs ? qcs[(size_t) qrc * LK_N_HEADS + head] : 0.0f;
-            qf8[qb] = ok ? qv : zi;
-            const float d = ok ? dv : 0.0f;
-            // scores are kept in units of 1/sq until the exponent (sq > 0 scales
-            // commute with the max); an all-zero query row has sq = 0 and zero
-            // int8 scores, so unit scaling is exact for it
-            sq[qb] = (d > 0.0f) ? d : 1.0f;
-            // exact tiles' score in units of 1/sq: (sum*log2e - qc) / sq as one fma
-            const float isq = 1.0f / sq[qb];
-            const float qc = ok ? cv : 0.0f;
-            exa[qb] = LK_LOG2E_F * isq;
-            exb[qb] = -qc * isq;
-        } else {
-            qf8[qb] = zi; sq[qb] = 1.0f; exa[qb] = LK_LOG2E_F; exb[qb] = 0.0f;
+            for (int i = 0; i < 8; ++i) {
+                const int qr = qbase + (lane >> 3) + 8 * i;
+                qv16[i] = *(const lk_h8 *) (qh + (size_t) (qr < m ? qr : m - 1) * LK_HIDDEN + head * LK_HEAD_DIM + 8 * (lane & 7));
+            }
         }
-    }
-    {
-        const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
+        // ---- int8 Q operands and per-query scalars (lane column = query) ------
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = (lane >> 3) + 8 * i;
-            *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * (lane & 7)) = (qbase + r < m) ? qv16[i] : z8;
+        for (int qb = 0; qb < PF_QB; ++qb) {
+            const int qr = qbase + 16 * qb + col;
+            const bool ok = qr < m;
+            const int qrc = ok ? qr : m - 1;              // clamped: unconditional loads
+            const lk_i4 zi = { 0, 0, 0, 0 };
+            if (INT8) {
+                const lk_i4 qv = *(const lk_i4 *) (q8 + (size_t) qrc * LK_HIDDEN + head * LK_HEAD_DIM + 16 * g);
+                const float dv = qsc[(size_t) qrc * LK_N_HEADS + head];
+                const float cv = qcs ? qcs[(size_t) qrc * LK_N_HEADS + head] : 0.0f;
+                qf8[qb] = ok ? qv : zi;
+                const float d = ok ? dv : 0.0f;
+                // scores are kept in units of 1/sq until the exponent (sq > 0
+                // scales commute with the max); an all-zero query row has sq = 0
+                // and zero int8 scores, so unit scaling is exact for it
+                sq[qb] = (d > 0.0f) ? d : 1.0f;
+                // exact tiles' score in units of 1/sq: (sum*log2e - qc) / sq as one fma
+                const float isq = 1.0f / sq[qb];
+                const float qc = ok ? cv : 0.0f;
+                exa[qb] = LK_LOG2E_F * isq;
+                exb[qb] = -qc * isq;
+            } else {
+                qf8[qb] = zi; sq[qb] = 1.0f; exa[qb] = LK_LOG2E_F; exb[qb] = 0.0f;
+            }
         }
-    }
+        if (fill_s_q) {
+            const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int r = (lane >> 3) + 8 * i;
+                *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * (lane & 7)) = (qbase + r < m) ? qv16[i] : z8;
+            }
+        }
+    };
+    load_q(true);
+    int qw = w;                                       // the s_q block exact tiles read
 
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
     // all-ones A operand, so every lane of query column q accumulates
@@ -484,6 +556,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // bodies specialised per mode (one loop each, or one loop with a branch to
     // each) measured 40% slower, the register allocator then spilled.
     auto tile = [&](const PfStage & S, int kt) {
+        // PAIR: two lane-derived offsets recomputed here (see dma_lane)
+        const int tl = dma_lane();
+        const int tcol = tl & 15, tg = tl >> 4;
         const int md = mode_of(kt);
         const bool msk = mask_of(kt);
         const int kb0 = kt * PF_BK;
@@ -492,15 +567,15 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         if (md != PF_EXACT) {
             // the scale pair of the tile's 64 keys, one key per lane, through
             // this wave's own LDS rows (LDS accesses of a wave complete in order)
-            const float s22 = lk_pf_ks22(S.ks[lane]);
-            s_kp[w][lane] = s22;
-            s_kp[w][PF_BK + lane] = s22 * -PF_MAGIC;
+            const float s22 = lk_pf_ks22(S.ks[tl]);
+            s_kp[w][tl] = s22;
+            s_kp[w][PF_BK + tl] = s22 * -PF_MAGIC;
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
-                ka[kb] = *(const lk_i4 *) (S.k8 + o_k8 + 1024 * kb);
-                sk[kb] = *(const lk_f4 *) (&s_kp[w][16 * kb + 4 * g]);
-                skb[kb] = *(const lk_f4 *) (&s_kp[w][PF_BK + 16 * kb + 4 * g]);
+                ka[kb] = *(const lk_i4 *) (S.k8 + (PAIR ? tcol * 64 + 16 * (tg ^ (tcol >> 2)) : o_k8) + 1024 * kb);
+                sk[kb] = *(const lk_f4 *) (&s_kp[w][16 * kb + 4 * tg]);
+                skb[kb] = *(const lk_f4 *) (&s_kp[w][PF_BK + 16 * kb + 4 * tg]);
             }
         }
         lk_h8 pb[PF_QB][2];
@@ -514,7 +589,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 lk_h8 qa[2][2];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int8_t * qrow = s_q[w] + o_q + 16 * PF_Q_LD * (2 * hq + j);
+                    const int8_t * qrow = s_q[qw] + o_q + 16 * PF_Q_LD * (2 * hq + j);
                     qa[j][0] = *(const lk_h8 *) qrow;
                     qa[j][1] = *(const lk_h8 *) (qrow + 64);
                 }
@@ -550,7 +625,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     // key kb0+16kb+4g+i is masked iff 16kb+i > qpos - kb0 - 4g
-                    const int dq = P + qbase + 16 * (2 * hq + j) + col - kb0 - 4 * g;
+                    const int dq = P + qbase + 16 * (2 * hq + j) + tcol - kb0 - 4 * tg;
 #pragma unroll
                     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -646,44 +721,115 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         }
     };
 
-    // ---- tile loop: one barrier per tile; tile kt+1 streams in while kt computes
-    for (int kt = kt_lo; kt < kt_hi; ++kt) {
-        lk_wait_vm<0>();                                  // this wave's part of tile kt landed
-        __syncthreads();                                  // ... everyone's; tile kt-1 fully consumed
-        if (kt + 1 < kt_hi) issue(kt + 1);                // into the stage tile kt-1 used
-        tile(st[kt & 1], kt);
-    }
-
-    if (pslot >= 0) {                                     // a part: unnormalised partial
-        float * R = pbuf + (size_t) (pslot * LK_N_KV_HEADS + kvh) * PF_PART_SLOT;
-        lk_f4 * A = (lk_f4 *) R + (size_t) w * 16 * PF_BQ;                 // [16 chunks][64 rows]
-        float2 * ML = (float2 *) (R + PF_PART_ACC) + w * PF_BQ;           // [64 rows]
+    // ---- epilogue: l over the 4 lane groups, then o[q][head*64 + d] -------------
+    auto emit = [&]() {
 #pragma unroll
         for (int qb = 0; qb < PF_QB; ++qb) {
-            const int row = 16 * qb + col;
+            const float il = 1.0f / acc[4][qb][0];
+            const int qr = qbase + 16 * qb + col;
+            lk_f4 a[4];
 #pragma unroll
-            for (int db = 0; db < 4; ++db) A[(4 * db + g) * PF_BQ + row] = acc[db][qb];
-            if (g == 0) ML[row] = make_float2(fmaf(mrun[qb], sq[qb], PF_P_BIAS), acc[4][qb][0]);
+            for (int db = 0; db < 4; ++db) a[db] = acc[db][qb] * il;
+            if (o && qr < m) {
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+                    *(float4 *) (o + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 16 * db + 4 * g) =
+                        make_float4(a[db][0], a[db][1], a[db][2], a[db][3]);
+            }
+            if (aqs) lk_pf_q81_epilogue(a, qr < m, aqs + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM,
+                                        asc + (size_t) qr * (LK_HIDDEN / 32) + 2 * head, g);
         }
-        return;
-    }
+    };
 
-    // ---- epilogue: l over the 4 lane groups, then o[q][head*64 + d] -------------
-#pragma unroll
-    for (int qb = 0; qb < PF_QB; ++qb) {
-        const float il = 1.0f / acc[4][qb][0];
-        const int qr = qbase + 16 * qb + col;
-        lk_f4 a[4];
-#pragma unroll
-        for (int db = 0; db < 4; ++db) a[db] = acc[db][qb] * il;
-        if (o && qr < m) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                *(float4 *) (o + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 16 * db + 4 * g) =
-                    make_float4(a[db][0], a[db][1], a[db][2], a[db][3]);
+    if constexpr (!PAIR) {
+        // ---- tile loop: one barrier per tile; tile kt+1 streams in while kt computes
+        for (int kt = kt_lo; kt < kt_hi; ++kt) {
+            lk_wait_vm<0>();                              // this wave's part of tile kt landed
+            __syncthreads();                              // ... everyone's; tile kt-1 fully consumed
+            if (kt + 1 < kt_hi) issue(kt + 1);            // into the stage tile kt-1 used
+            tile(st[kt & 1], kt);
         }
-        if (aqs) lk_pf_q81_epilogue(a, qr < m, aqs + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM,
-                                    asc + (size_t) qr * (LK_HIDDEN / 32) + 2 * head, g);
+
+        if (pslot >= 0) {                                 // a part: unnormalised partial
+            float * R = pbuf + (size_t) (pslot * LK_N_KV_HEADS + kvh) * PF_PART_SLOT;
+            lk_f4 * A = (lk_f4 *) R + (size_t) w * 16 * PF_BQ;             // [16 chunks][64 rows]
+            float2 * ML = (float2 *) (R + PF_PART_ACC) + w * PF_BQ;       // [64 rows]
+#pragma unroll
+            for (int qb = 0; qb < PF_QB; ++qb) {
+                const int row = 16 * qb + col;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) A[(4 * db + g) * PF_BQ + row] = acc[db][qb];
+                if (g == 0) ML[row] = make_float2(fmaf(mrun[qb], sq[qb], PF_P_BIAS), acc[4][qb][0]);
+            }
+            return;
+        }
+        emit();
+    } else {
+        // ---- step loop: steps 0 .. nki-1 take tile `it` for both blocks (group A
+        // bi, group B bj); the later steps take two tiles of bj, one per group.
+        // One barrier per step; step it+1's tiles stream in during step it.
+        // Without a2 the later steps take one tile each, group B's.
+        const int nsteps = a2 ? nki + (nkj - nki + 1) / 2 : nkj;
+        for (int it = 0; it < nsteps; ++it) {
+            lk_wait_vm<0>();
+            __syncthreads();
+            if (it + 1 < nsteps) issue_step(it + 1);
+            const bool both = it < nki;
+            const int kt = both ? it : a2 ? nki + 2 * (it - nki) + grp : (grp == 1 ? it : nkj);
+            if (kt < nkj) tile(st[2 * (it & 1) + (both ? 0 : grp)], kt);
+            if (both) {
+                if (grp == 0 && it == nki - 1) {
+                    // bi is complete: write it; group A continues on bj, whose
+                    // fp16 Q block group B's wave of the same head holds in LDS
+                    emit();
+                    qt = bj;
+                    qbase = bj * PF_BQ;
+                    qw = hw + 4;
+                    load_q(false);
+#pragma unroll
+                    for (int db = 0; db < 5; ++db)
+#pragma unroll
+                        for (int qb = 0; qb < PF_QB; ++qb) acc[db][qb] = (lk_f4){ 0.f, 0.f, 0.f, 0.f };
+#pragma unroll
+                    for (int qb = 0; qb < PF_QB; ++qb) mrun[qb] = -INFINITY;
+                }
+            }
+        }
+        // ---- group A's part of bj into group B's, through LDS (the tile stages
+        // are free now), in the split-partial layout; lane l of wave hw+4 reads
+        // exactly what lane l of wave hw wrote.  Fixed order: B's part, then A's.
+        __syncthreads();
+        float * R = (float *) &st[0];
+        lk_f4 * A = (lk_f4 *) R + (size_t) hw * 16 * PF_BQ;
+        float2 * ML = (float2 *) (R + PF_PART_ACC) + hw * PF_BQ;
+        if (grp == 0) {
+#pragma unroll
+            for (int qb = 0; qb < PF_QB; ++qb) {
+                const int row = 16 * qb + col;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) A[(4 * db + g) * PF_BQ + row] = acc[db][qb];
+                ML[row] = make_float2(fmaf(mrun[qb], sq[qb], PF_P_BIAS), acc[4][qb][0]);
+            }
+        }
+        __syncthreads();
+        if (grp == 1) {
+#pragma clang fp contract(off)
+#pragma unroll
+            for (int qb = 0; qb < PF_QB; ++qb) {
+                const int row = 16 * qb + col;
+                const float2 ml = ML[row];
+                const float mb = fmaf(mrun[qb], sq[qb], PF_P_BIAS);
+                const float mx = fmaxf(mb, ml.x);
+                const float fb = lk_exp2(mb - mx), fa = lk_exp2(ml.x - mx);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) {
+                    const lk_f4 pa = A[(4 * db + g) * PF_BQ + row];
+                    acc[db][qb] = acc[db][qb] * fb + pa * fa;
+                }
+                acc[4][qb][0] = acc[4][qb][0] * fb + ml.y * fa;
+            }
+            emit();
+        }
     }
 }
 
@@ -1058,15 +1204,49 @@ extern "C" int lk_pf_plan_items(int m, int P, int near, int sink, int int8, int3
     return wk.n_items;
 }
 
+// Paired launches (8-wave workgroups over blocks i and nq-1-i): -1 never,
+// 0 automatic, 1 whenever the chunk has at least two query blocks (test hook).
+static int g_pf_pair_override = 0;
+
+extern "C" int lk_pf_pair_override(int mode) {
+    if (mode < -1 || mode > 1) return lk_fail(hipErrorInvalidValue, "lk_pf_pair_override: %d not in -1..1", mode);
+    g_pf_pair_override = mode;
+    return 0;
+}
+
+// Automatic choice: the fp16 kernel on chunks of at least 64 query blocks
+// (4096 rows, one paired workgroup per CU) with P <= m, where the causal
+// triangle dominates the work (4096-row chunk: 99.4 us against 111.5 unpaired
+// at P = 0, 263.6 against 272.5 at P = 4096).  Deeper chunks keep the split
+// plan (P = 16384: 682.5 paired against 637.3).  Not the int8 kernel: its two
+// groups run the same phase in lockstep (int8 Q.K^T beside int8 Q.K^T,
+// softmax beside softmax), where two unpaired workgroups per CU drift into
+// different phases and overlap MFMA with VALU; paired it measured 111.9 us
+// against 109.2 at P = 0.  Not under a forced split size.
+static bool pf_use_pair(int m, int P, bool int8) {
+    const int nq = (m + PF_BQ - 1) / PF_BQ;
+    if (g_pf_pair_override < 0 || nq < 2) return false;
+    if (g_pf_pair_override > 0) return true;
+    return g_pf_split_override <= 0 && !int8 && P <= m && nq >= 64;
+}
+
 template <bool INT8>
 static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qcs, const _Float16 * qh,
                           int m, int P, const int8_t * k8, const float * ksc, int kstride,
                           const _Float16 * kc, const _Float16 * vc, int near, int sink, float * o,
                           int8_t * aqs, float2 * asc, hipStream_t st, const char * what) {
     PfWork wk;
+    if (pf_use_pair(m, P, INT8)) {
+        wk.n_items = 0; wk.n_split = 0;
+        const int npairs = ((m + PF_BQ - 1) / PF_BQ + 1) / 2;
+        hipLaunchKernelGGL((lk_k_pf_attn<INT8, true>), dim3(npairs * LK_N_KV_HEADS), dim3(512), 0, st,
+                           q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk,
+                           (float *) nullptr);
+        return lk_launch_status(what);
+    }
     pf_plan(m, P, near, sink, INT8, wk);
     if (wk.n_items == 0) {
-        hipLaunchKernelGGL(lk_k_pf_attn<INT8>, dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0, st,
+        hipLaunchKernelGGL((lk_k_pf_attn<INT8, false>), dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0, st,
                            q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk,
                            (float *) nullptr);
         return lk_launch_status(what);
@@ -1074,7 +1254,7 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
     int err = 0, dev = 0;
     float * pbuf = pf_part_acquire(st, err, dev);
     if (!pbuf) return err;
-    hipLaunchKernelGGL(lk_k_pf_attn<INT8>, dim3(wk.n_items * LK_N_KV_HEADS), dim3(256), 0, st,
+    hipLaunchKernelGGL((lk_k_pf_attn<INT8, false>), dim3(wk.n_items * LK_N_KV_HEADS), dim3(256), 0, st,
                        q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk, pbuf);
     int rc = lk_launch_status(what);
     if (rc) return rc;

@@ -28,7 +28,7 @@ EXPORTS = (
     "lk_attn_split", "lk_attn_combine", "lk_attn_decode", "lk_attention_decode",
     "lk_decode_graph_create", "lk_decode_graph_launch", "lk_decode_graph_nodes",
     "lk_decode_graph_destroy",
-    "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_split_override",
+    "lk_pf_q8", "lk_pf_k8", "lk_pf_kmean", "lk_pf_attn8", "lk_pf_attn", "lk_pf_split_override", "lk_pf_pair_override",
     "lk_pf_qk_i32", "lk_pf_plan_items", "lk_read_probe", "lk_qk_norm_rope", "lk_pf_qknr",
     "lk_decode_step_graph_create", "lk_decode_graph_run",
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
@@ -78,6 +78,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_attn8": ([P, P, P, P, I, I, P, P, I, P, P, I, I, P, P], I),
         "lk_pf_attn": ([P, I, I, P, P, P, P], I),
         "lk_pf_split_override": ([I], I),
+        "lk_pf_pair_override": ([I], I),
         "lk_pf_qk_i32": ([P, I, P, I, P, P], I),
         "lk_pf_plan_items": ([I, I, I, I, I, P, I], I),
         "lk_read_probe": ([P, S, P, P], I),
@@ -309,6 +310,12 @@ def pf_attn_q81(qh, m, P, kc, vc, o, aqs, asc, stream=None) -> None:
 def pf_quant_rows(X, rows, ld, kb, qs, sc, stream=None) -> None:
     _check(load().lk_pf_quant_rows(_ptr(X), int(rows), int(ld), int(kb), _ptr(qs), _ptr(sc), _stream(stream)),
            "lk_pf_quant_rows")
+
+
+def pf_pair_override(mode: int) -> None:
+    """Paired prefill workgroups (blocks i and nq-1-i in one launch unit):
+    -1 never, 0 automatic, 1 whenever the chunk has at least two 64-row blocks."""
+    _check(load().lk_pf_pair_override(int(mode)), "lk_pf_pair_override")
 
 
 def pf_split_override(tiles: int) -> None:

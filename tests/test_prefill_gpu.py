@@ -226,6 +226,59 @@ def test_attn_split_parts(lk, oracle, m, P, near, L):
     assert np.array_equal(again8.view(np.uint32), part8.view(np.uint32))
 
 
+# ---- paired workgroups (blocks i and nq-1-i in one 8-wave workgroup) ----------------------------
+PAIR_CASES = [
+    # (m, P, near): nq 2 (adjacent blocks); nq 3 ragged (the middle block alone);
+    # nq 4 with P % 64 != 0 (the adjacent middle pair's later tiles all on one
+    # group); nq 5 ragged; nq 8 deep; mixed exact/int8 tiles, sink on
+    (128, 0, 0),
+    (130, 0, 96),
+    (256, 1, 96),
+    (300, 37, 96),
+    (500, 700, 1024),
+    (129, 2000, 1024),
+]
+
+
+@pytest.mark.parametrize("m,P,near", PAIR_CASES, ids=[f"m{c[0]}_P{c[1]}_n{c[2]}" for c in PAIR_CASES])
+def test_attn_pair(lk, oracle, m, P, near):
+    """Paired launches, forced: both kernels against their float64 references
+    and against the unpaired launch (bj's key range is cut in two parts and
+    merged, so the same tolerance class as split parts), bit-identical on
+    repeat, and the fused Q8_1 planes equal to quantising the float output."""
+    K, V, Q = _inputs(oracle, m, P, 1.0, True)
+    sink = int(near > 0)
+    note(f"pf pair m={m} P={P} near={near}")
+    d = _Dev(lk, K, V, Q, m, P, False)
+    aqs = torch.zeros(m, 2048, dtype=torch.int8, device="cuda")
+    asc = torch.zeros(m, 64, 2, device="cuda")
+    try:
+        lk.pf_pair_override(-1)
+        whole8, whole16 = d.attn8(lk, near, sink), d.attn16(lk)
+        lk.pf_pair_override(1)
+        pair8, pair16 = d.attn8(lk, near, sink), d.attn16(lk)
+        again8, again16 = d.attn8(lk, near, sink), d.attn16(lk)
+        o = torch.full((m, 2048), float("nan"), device="cuda")
+        lk.pf_attn_q81(d.qh, m, P, d.kc, d.vc, o, aqs, asc)
+        torch.cuda.synchronize()
+    finally:
+        lk.pf_pair_override(0)
+    ref8 = oracle.pf_ref8(host(d.q8), host(d.qsc), host(d.qcs), Q, m, P, host(d.k8), host(d.ksc),
+                          d.kstride, K, V, near, sink)
+    ref = oracle.pf_ref(Q, m, P, K, V)
+    r8, r16 = oracle.rel_err(pair8, ref8), oracle.rel_err(pair16, ref)
+    d8, d16 = oracle.rel_err(pair8, whole8), oracle.rel_err(pair16, whole16)
+    note(f"  pair: int8 rel {r8:.3e}, fp16 rel {r16:.3e}; vs unpaired rel {d8:.3e} / {d16:.3e}")
+    assert r8 <= 2e-3 and r16 <= 2e-3 and abs_err(pair16, ref) <= 4e-3
+    assert d8 <= 1e-3 and d16 <= 1e-3
+    assert np.isfinite(pair8).all() and np.isfinite(pair16).all()
+    assert np.array_equal(again8.view(np.uint32), pair8.view(np.uint32))
+    assert np.array_equal(again16.view(np.uint32), pair16.view(np.uint32))
+    assert np.array_equal(host(o).view(np.uint32), pair16.view(np.uint32))
+    qso, sco = oracle.pf_quant_rows(host(o), m, 2048, 64)
+    assert np.array_equal(host(aqs), qso) and np.array_equal(host(asc).view(np.uint32), sco.view(np.uint32))
+
+
 # ---- the automatic (cost-model) split plan ------------------------------------------------------
 AUTO_CASES = [(1000, 0, 256), (777, 0, 1024), (1500, 300, 96), (2048, 777, 1024), (4096, 4096, 1024),
               (512, 8000, 1024), (300, 20000, 256)]          # short chunks deep in a prompt: few blocks
