@@ -241,13 +241,13 @@ int lk_pf_quant_rows(const float * X, int rows, int ld, int kb, int8_t * qs, flo
 int lk_pf_split_override(int tiles);
 
 /* Paired launches: one 8-wave workgroup per (kv head, block pair i, nq-1-i) of
- * a chunk, the two 4-wave halves sharing the key tiles block i sees, then
- * splitting the rest of block nq-1-i between them (merged in LDS, fixed order).
- * Every workgroup does the same work, so a 4096-row chunk at P = 0 needs no
- * split.  Process-wide knob, for tests and tuning: -1 never, 0 automatic
- * (default: the fp16 kernel on chunks of at least 64 blocks with P <= m), 1
- * whenever the chunk has two or more blocks (both kernels).  No counterpart in
- * the reference. */
+ * a chunk; one 4-wave half scores block i and the first part of block
+ * nq-1-i, the other half the rest of it, and the two parts are merged in LDS
+ * (fixed order).  Every workgroup does the same work, so a 4096-row chunk at
+ * P = 0 needs no split.  Process-wide knob, for tests and tuning: -1 never,
+ * 0 automatic (default: chunks of at least 64 blocks with P <= m), 1
+ * whenever the chunk has two or more blocks.  No counterpart in the
+ * reference. */
 int lk_pf_pair_override(int mode);
 
 /* ---- attention-input producers ---------------------------------------------

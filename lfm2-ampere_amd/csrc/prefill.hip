@@ -272,13 +272,15 @@ __device__ __forceinline__ void lk_pf_q81_epilogue(const lk_f4 (&a)[4], bool sto
 }
 
 // PAIR: workgroups of 8 waves, each over query blocks bi = pair index and
-// bj = nq-1-bi of one kv head.  Waves 0-3 (group A) and 4-7 (group B) share
-// one key-tile stream: while both blocks see the tile (keys of block bi's
-// range) group A scores it for bi and group B for bj; the rest of bj's tiles
-// alternate between the groups, two tiles per step, and at the end group A's
-// part of bj is merged into group B's through LDS.  Every workgroup then
+// bj = nq-1-bi of one kv head.  Waves 0-3 (group A) take bi and then bj's
+// key tiles [0, xs); waves 4-7 (group B) take bj's tiles [xs, nkj); xs is
+// chosen so that both groups score about the same number of tiles, and at the
+// end A's part of bj is merged into B's through LDS.  Every workgroup then
 // does the same work (about half of bi + bj), with no split-K partials in
-// memory and no merge kernel.
+// memory and no merge kernel.  The groups stream their own tiles and meet at
+// barriers of their own (a counter in LDS), not at the workgroup barrier, so
+// the two waves of a SIMD (one per group) drift into different phases of
+// their tiles, as two unpaired workgroups do.
 template <bool INT8, bool PAIR>
 __global__ void __launch_bounds__(PAIR ? 512 : 256, PAIR ? 1 : 2)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
@@ -303,8 +305,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     const int col  = lane & 15, g = lane >> 4;
     const int hw   = w & 3, grp = w >> 2;                 // head within the kv head; PAIR group
     int kvh, qt, kt_lo, kt_hi, pslot = -1;
-    int bi = 0, bj = 0, nki = 0, nkj = 0;                 // PAIR: the two blocks, their tile counts
-    bool a2 = true;                                       // PAIR: group A takes half of bj's later tiles
+    int bi = 0, bj = 0, nki = 0, nkj = 0, xs = 0;         // PAIR: the two blocks, their tile counts, the cut of bj
     if constexpr (PAIR) {
         kvh = blockIdx.x % LK_N_KV_HEADS;
         const int nq = (m + PF_BQ - 1) / PF_BQ;
@@ -312,11 +313,13 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         bj = nq - 1 - bi;
         nki = (bi == bj) ? 0 : pf_nkt(bi, m, P);
         nkj = pf_nkt(bj, m, P);
-        // Group A's first tile of bj (tile nki) must hold a key that every row
-        // of bj sees, or a row would start A's part with no visible key; only
-        // bj = bi+1 with P not a multiple of 64 breaks that, and then group B
-        // takes all of bj's remaining tiles.
-        a2 = nki == 0 || nki * PF_BK <= P + bj * PF_BQ;
+        // nki + xs = nkj - xs balances the groups; B's first tile must not lie
+        // past bj's first query, so that every row of bj sees a key in B's part
+        // (A's part starts at key 0)
+        xs = (nkj - nki) / 2;
+        const int kdj = (P + bj * PF_BQ) / PF_BK;
+        if (xs > kdj) xs = kdj;
+        if (xs < 0) xs = 0;
         qt = (grp == 0 && nki > 0) ? bi : bj;             // group A starts on bi when it has one
         kt_lo = 0; kt_hi = 0;
     } else if (work.n_items == 0) {
@@ -354,9 +357,11 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     const int ks_clamp = ((kend - 1) / 4) * 4;        // last 16-byte chunk holding a visible key
     // Per-lane byte offsets of the DMA sources relative to the tile's first key
     // (the kv head folded in); the tile base itself is wave-uniform.
-    // PAIR: the offsets are recomputed at each issue from an opaque copy of
-    // the lane id (the compiler would otherwise keep five of them live across
-    // the loop, at a register budget that leaves no room for them).
+    // PAIR: these offsets (and the Q addresses of load_q below) are formed at
+    // each use from an opaque copy of the lane id; the compiler would
+    // otherwise form them once and keep them live across the tile loop, at a
+    // register budget that leaves no room for them (spills, and every reload
+    // waits for the tile DMA in flight).
     auto dma_lane = [&]() -> int {
         if constexpr (PAIR) {
             int l;
@@ -429,29 +434,41 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     };
 
     auto issue = [&](int kt) { issue_to(kt, kt & 1, mode_of(kt)); };
-    // PAIR: the tiles of step it (one tile both groups read, then two tiles,
-    // one per group, into the step's two slots); waves 0-3 fetch slot 0,
-    // waves 4-7 slot 1
+    // PAIR: step it of the wave's group: A bi's tiles then bj's [0, xs), B
+    // bj's [xs, nkj); each group double-buffers in its own two stages
+    const int g_ns = (grp == 0) ? nki + xs : nkj - xs;   // steps of the wave's group
+    auto g_tile = [&](int it) -> int { return (grp == 0) ? (it < nki ? it : it - nki) : xs + it; };
+    auto g_base = [&](int it) -> int { return (grp == 0 && it < nki) ? bi * PF_BQ : bj * PF_BQ; };
     auto issue_step = [&](int it) {
-        const int si = 2 * (it & 1);
-        if (it < nki) {
-            if (grp == 0) {
-                const int ma = mode_at(it, bi * PF_BQ);
-                const int mb = mode_at(it, bj * PF_BQ);
-                const bool n8 = ma != PF_EXACT || mb != PF_EXACT, n16 = ma != PF_INT8 || mb != PF_INT8;
-                issue_to(it, si, n8 ? (n16 ? PF_MIXED : PF_INT8) : PF_EXACT);
-            }
-        } else if (a2) {
-            const int kt = nki + 2 * (it - nki) + grp;
-            if (kt < nkj) issue_to(kt, si + grp, mode_at(kt, bj * PF_BQ));
-        } else if (grp == 1) {
-            issue_to(it, si + 1, mode_at(it, bj * PF_BQ));
-        }
+        const int kt = g_tile(it);
+        issue_to(kt, 2 * grp + (it & 1), mode_at(kt, g_base(it)));
     };
+    // PAIR: the group barrier, a counter per group in LDS that only grows
+    // (4 arrivals per step); the poll is bounded so that a wave can never
+    // hang the kernel.
+    __shared__ unsigned s_gbar[2];
+    unsigned g_gen = 0;
+    auto gsync = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) __hip_atomic_fetch_add(&s_gbar[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        g_gen += 4;
+        for (int n = 0; n < (1 << 22); ++n) {
+            const unsigned c = __builtin_amdgcn_readfirstlane(
+                __hip_atomic_load(&s_gbar[grp], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            if ((int) (c - g_gen) >= 0) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    };
+    if constexpr (PAIR) {
+        if (tid < 2) s_gbar[tid] = 0u;
+        // (the workgroup barrier after the Q prologue below orders this
+        // before every group barrier)
+    }
 
     // The first tile's DMA goes out before the Q loads below, so that the two
     // memory latencies overlap.
-    if constexpr (PAIR) issue_step(0);
+    if constexpr (PAIR) { if (g_ns > 0) issue_step(0); }
     else issue(kt_lo);
 
     // ---- this wave's fp16 Q block (64 rows x 128 B), for exact tiles, and the
@@ -471,14 +488,18 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             }
         }
         // ---- int8 Q operands and per-query scalars (lane column = query) ------
+        // (PAIR: the lane id through dma_lane, so that the addresses of the
+        // second call are not formed early and kept live across the tiles)
+        const int lq = dma_lane();
+        const int qcol = lq & 15, qg = lq >> 4;
 #pragma unroll
         for (int qb = 0; qb < PF_QB; ++qb) {
-            const int qr = qbase + 16 * qb + col;
+            const int qr = qbase + 16 * qb + qcol;
             const bool ok = qr < m;
             const int qrc = ok ? qr : m - 1;              // clamped: unconditional loads
             const lk_i4 zi = { 0, 0, 0, 0 };
             if (INT8) {
-                const lk_i4 qv = *(const lk_i4 *) (q8 + (size_t) qrc * LK_HIDDEN + head * LK_HEAD_DIM + 16 * g);
+                const lk_i4 qv = *(const lk_i4 *) (q8 + (size_t) qrc * LK_HIDDEN + head * LK_HEAD_DIM + 16 * qg);
                 const float dv = qsc[(size_t) qrc * LK_N_HEADS + head];
                 const float cv = qcs ? qcs[(size_t) qrc * LK_N_HEADS + head] : 0.0f;
                 qf8[qb] = ok ? qv : zi;
@@ -506,6 +527,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         }
     };
     load_q(true);
+    // PAIR: every wave's s_q block (group A reads group B's for bj) and the
+    // group counters are in place before any group goes on
+    if constexpr (PAIR) __syncthreads();
     int qw = w;                                       // the s_q block exact tiles read
 
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
@@ -556,9 +580,6 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // bodies specialised per mode (one loop each, or one loop with a branch to
     // each) measured 40% slower, the register allocator then spilled.
     auto tile = [&](const PfStage & S, int kt) {
-        // PAIR: two lane-derived offsets recomputed here (see dma_lane)
-        const int tl = dma_lane();
-        const int tcol = tl & 15, tg = tl >> 4;
         const int md = mode_of(kt);
         const bool msk = mask_of(kt);
         const int kb0 = kt * PF_BK;
@@ -567,15 +588,15 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         if (md != PF_EXACT) {
             // the scale pair of the tile's 64 keys, one key per lane, through
             // this wave's own LDS rows (LDS accesses of a wave complete in order)
-            const float s22 = lk_pf_ks22(S.ks[tl]);
-            s_kp[w][tl] = s22;
-            s_kp[w][PF_BK + tl] = s22 * -PF_MAGIC;
+            const float s22 = lk_pf_ks22(S.ks[lane]);
+            s_kp[w][lane] = s22;
+            s_kp[w][PF_BK + lane] = s22 * -PF_MAGIC;
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
-                ka[kb] = *(const lk_i4 *) (S.k8 + (PAIR ? tcol * 64 + 16 * (tg ^ (tcol >> 2)) : o_k8) + 1024 * kb);
-                sk[kb] = *(const lk_f4 *) (&s_kp[w][16 * kb + 4 * tg]);
-                skb[kb] = *(const lk_f4 *) (&s_kp[w][PF_BK + 16 * kb + 4 * tg]);
+                ka[kb] = *(const lk_i4 *) (S.k8 + o_k8 + 1024 * kb);
+                sk[kb] = *(const lk_f4 *) (&s_kp[w][16 * kb + 4 * g]);
+                skb[kb] = *(const lk_f4 *) (&s_kp[w][PF_BK + 16 * kb + 4 * g]);
             }
         }
         lk_h8 pb[PF_QB][2];
@@ -625,7 +646,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     // key kb0+16kb+4g+i is masked iff 16kb+i > qpos - kb0 - 4g
-                    const int dq = P + qbase + 16 * (2 * hq + j) + tcol - kb0 - 4 * tg;
+                    const int dq = P + qbase + 16 * (2 * hq + j) + col - kb0 - 4 * g;
 #pragma unroll
                     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -765,34 +786,27 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         }
         emit();
     } else {
-        // ---- step loop: steps 0 .. nki-1 take tile `it` for both blocks (group A
-        // bi, group B bj); the later steps take two tiles of bj, one per group.
-        // One barrier per step; step it+1's tiles stream in during step it.
-        // Without a2 the later steps take one tile each, group B's.
-        const int nsteps = a2 ? nki + (nkj - nki + 1) / 2 : nkj;
-        for (int it = 0; it < nsteps; ++it) {
+        // ---- the group's step loop: one group barrier per step; step it+1's
+        // tile streams in during step it
+        for (int it = 0; it < g_ns; ++it) {
             lk_wait_vm<0>();
-            __syncthreads();
-            if (it + 1 < nsteps) issue_step(it + 1);
-            const bool both = it < nki;
-            const int kt = both ? it : a2 ? nki + 2 * (it - nki) + grp : (grp == 1 ? it : nkj);
-            if (kt < nkj) tile(st[2 * (it & 1) + (both ? 0 : grp)], kt);
-            if (both) {
-                if (grp == 0 && it == nki - 1) {
-                    // bi is complete: write it; group A continues on bj, whose
-                    // fp16 Q block group B's wave of the same head holds in LDS
-                    emit();
-                    qt = bj;
-                    qbase = bj * PF_BQ;
-                    qw = hw + 4;
-                    load_q(false);
+            gsync();
+            if (it + 1 < g_ns) issue_step(it + 1);
+            tile(st[2 * grp + (it & 1)], g_tile(it));
+            if (grp == 0 && it == nki - 1) {
+                // bi is complete: write it; group A goes on with bj, whose fp16
+                // Q block group B's wave of the same head holds in LDS
+                emit();
+                qt = bj;
+                qbase = bj * PF_BQ;
+                qw = hw + 4;
+                load_q(false);
 #pragma unroll
-                    for (int db = 0; db < 5; ++db)
+                for (int db = 0; db < 5; ++db)
 #pragma unroll
-                        for (int qb = 0; qb < PF_QB; ++qb) acc[db][qb] = (lk_f4){ 0.f, 0.f, 0.f, 0.f };
+                    for (int qb = 0; qb < PF_QB; ++qb) acc[db][qb] = (lk_f4){ 0.f, 0.f, 0.f, 0.f };
 #pragma unroll
-                    for (int qb = 0; qb < PF_QB; ++qb) mrun[qb] = -INFINITY;
-                }
+                for (int qb = 0; qb < PF_QB; ++qb) mrun[qb] = -INFINITY;
             }
         }
         // ---- group A's part of bj into group B's, through LDS (the tile stages
@@ -1214,20 +1228,18 @@ extern "C" int lk_pf_pair_override(int mode) {
     return 0;
 }
 
-// Automatic choice: the fp16 kernel on chunks of at least 64 query blocks
-// (4096 rows, one paired workgroup per CU) with P <= m, where the causal
-// triangle dominates the work (4096-row chunk: 99.4 us against 111.5 unpaired
-// at P = 0, 263.6 against 272.5 at P = 4096).  Deeper chunks keep the split
-// plan (P = 16384: 682.5 paired against 637.3).  Not the int8 kernel: its two
-// groups run the same phase in lockstep (int8 Q.K^T beside int8 Q.K^T,
-// softmax beside softmax), where two unpaired workgroups per CU drift into
-// different phases and overlap MFMA with VALU; paired it measured 111.9 us
-// against 109.2 at P = 0.  Not under a forced split size.
-static bool pf_use_pair(int m, int P, bool int8) {
+// Automatic choice: chunks of at least 64 query blocks (4096 rows, one paired
+// workgroup per CU) with P <= m, where the causal triangle dominates the work.
+// Measured (repetitions alternating, 4096-row chunks): P = 0 int8 103.4 us
+// against 110.8 unpaired (split plan + combine), fp16 95.2 against 112.4;
+// P = 4096 int8 265.7 against 271.5, fp16 254.1 against 279.5.  Deep chunks
+// keep the split plan (P = 126976: int8 4383 us paired against 3862, fp16
+// 4397 against 4173).  Not under a forced split size.
+static bool pf_use_pair(int m, int P) {
     const int nq = (m + PF_BQ - 1) / PF_BQ;
     if (g_pf_pair_override < 0 || nq < 2) return false;
     if (g_pf_pair_override > 0) return true;
-    return g_pf_split_override <= 0 && !int8 && P <= m && nq >= 64;
+    return g_pf_split_override <= 0 && P <= m && nq >= 64;
 }
 
 template <bool INT8>
@@ -1236,7 +1248,7 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
                           const _Float16 * kc, const _Float16 * vc, int near, int sink, float * o,
                           int8_t * aqs, float2 * asc, hipStream_t st, const char * what) {
     PfWork wk;
-    if (pf_use_pair(m, P, INT8)) {
+    if (pf_use_pair(m, P)) {
         wk.n_items = 0; wk.n_split = 0;
         const int npairs = ((m + PF_BQ - 1) / PF_BQ + 1) / 2;
         hipLaunchKernelGGL((lk_k_pf_attn<INT8, true>), dim3(npairs * LK_N_KV_HEADS), dim3(512), 0, st,
