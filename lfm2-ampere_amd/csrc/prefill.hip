@@ -540,9 +540,13 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     for (int db = 0; db < 5; ++db)
 #pragma unroll
         for (int qb = 0; qb < PF_QB; ++qb) acc[db][qb] = (lk_f4){ 0.f, 0.f, 0.f, 0.f };
-    float mrun[PF_QB];                      // running max, units of 1/sq
+    // Per query, p = 2^(x*sq - moff) with the exponent offset moff = m*sq +
+    // PF_P_BIAS for a running max m (score units), -inf before the first
+    // tile.  mst holds m (unpaired launches) or moff itself (PAIR, whose
+    // rescale below moves moff by whole powers of two).
+    float mst[PF_QB];
 #pragma unroll
-    for (int qb = 0; qb < PF_QB; ++qb) mrun[qb] = -INFINITY;
+    for (int qb = 0; qb < PF_QB; ++qb) mst[qb] = -INFINITY;
     const _Float16 one = (_Float16) 1.0f;
     const lk_h8 ones = { one, one, one, one, one, one, one, one };
     // The running max is only raised when a score exceeds it by more than
@@ -563,6 +567,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 #endif
     constexpr float PF_P_BIAS = (float) PF_PBIAS;
     constexpr float PF_HEADROOM = PF_P_BIAS + 1.0f;
+    auto moff = [&](int qb) -> float { return PAIR ? mst[qb] : fmaf(mst[qb], sq[qb], PF_P_BIAS); };
 
     // ---- per-lane LDS read offsets: the swizzles above depend only on the lane
     // here, so every read below is one of these bases plus a constant.
@@ -654,26 +659,43 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                             if (16 * kb + i > dq) x[kb][j][i] = -INFINITY;
                 }
             }
-            // ---- online softmax, per query (lane column); exponent = sq*(x - m) - bias
-            // p is formed against the running max first.  The exact tile max is
-            // only needed when some score passes the headroom (or the max is
-            // still -inf: first tile): that is bit 14 of an fp16 p (p >= 2,
+            // ---- online softmax, per query (lane column); p = 2^(x*sq - moff)
+            // p is formed against the running offset first.  The exact tile max
+            // is only needed when some score passes the headroom (or the max
+            // is still -inf: first tile): that is bit 14 of an fp16 p (p >= 2,
             // inf or NaN), found in the OR of the p words, with no cross-lane
             // reduction.
             auto make_p = [&]() {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int qb = 2 * hq + j;
-                    const float msq = fmaf(mrun[qb], sq[qb], PF_P_BIAS);
+                    const float mo = moff(qb);
 #pragma unroll
                     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -msq));
-                            pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -msq));
+                            pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -mo));
+                            pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -mo));
                         }
                 }
             };
+            auto row_max = [&](int j) -> float {
+                float v = x[0][j][0];
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v = fmaxf(v, x[kb][j][i]);
+                return lk_xrow_max(v);                         // the 4 lane groups of this query
+            };
+            if constexpr (PAIR) {
+                // a part's first tile (every query at -inf: wave-uniform): the
+                // offset from the exact tile max before any p is formed (every
+                // query sees a key in it, so the max is finite)
+                if (__builtin_amdgcn_readfirstlane(__float_as_int(mst[2 * hq])) == __float_as_int(-INFINITY)) {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) mst[2 * hq + j] = fmaf(row_max(j), sq[2 * hq + j], PF_P_BIAS);
+                }
+            }
             // Wave priorities by phase: exponent pass 2, int8 Q.K^T and the
             // rest of the softmax 1, P.V 0.  The two waves of a SIMD (one per
             // co-resident workgroup) then tend to be in different phases, VALU
@@ -692,9 +714,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    const lk_i4 u = __builtin_bit_cast(lk_i4, pb[2 * hq + j][kk]);
+                    const lk_i4 uw = __builtin_bit_cast(lk_i4, pb[2 * hq + j][kk]);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) pw[8 * j + 4 * kk + e] = (unsigned) u[e];
+                    for (int e = 0; e < 4; ++e) pw[8 * j + 4 * kk + e] = (unsigned) uw[e];
                 }
 #pragma unroll
             for (int n = 16; n > 1; n = (n + 2) / 3)                // OR tree, three words per op
@@ -702,23 +724,68 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 for (int t = 0; t < (n + 2) / 3; ++t)
                     pw[t] = pw[3 * t] | (3 * t + 1 < n ? pw[3 * t + 1] : 0u) | (3 * t + 2 < n ? pw[3 * t + 2] : 0u);
             if (__ballot(pw[0] & 0x40004000u)) {               // wave-uniform, rare
+                if constexpr (PAIR) {
+                    // Raise the offset of the queries whose max passed the
+                    // headroom (u = max*sq - moff > PF_HEADROOM - PF_P_BIAS) by
+                    // the integer k = floor(u + PF_P_BIAS): their p (fp16, below
+                    // 2^15 while u <= 14) and acc then scale by exactly 2^-k, one
+                    // packed fp16 multiply per two p instead of forming them
+                    // again, and the largest p lands in [2^-PF_P_BIAS,
+                    // 2^(1-PF_P_BIAS)), at least as far from fp16's subnormals
+                    // as p formed against the exact max.  Past u = 14 (a p at
+                    // fp16's limit) the offset becomes max*sq + PF_P_BIAS and
+                    // that query block's p are formed again.  Shallow chunks
+                    // (the paired launches) rescale in 10-45% of the query
+                    // halves, deep ones in about 1.5%.
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int qb = 2 * hq + j;
-                    float v = x[0][j][0];
+                    for (int j = 0; j < 2; ++j) {
+                        const int qb = 2 * hq + j;
+                        const float mx = row_max(j);
+                        const float u = fmaf(mx, sq[qb], -mst[qb]);
+                        const bool need = u > PF_HEADROOM - PF_P_BIAS;
+                        if (__ballot(u > 14.0f)) {
+                            const float mn = need ? fmaf(mx, sq[qb], PF_P_BIAS) : mst[qb];
+                            const float alpha = need ? lk_exp2(mst[qb] - mn) : 1.0f;
+                            mst[qb] = mn;
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb)
+                            for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) v = fmaxf(v, x[kb][j][i]);
-                    const float mx = lk_xrow_max(v);           // the 4 lane groups of this query
-                    // key 0 is visible to every query, so mrun is finite after tile 0
-                    const bool need = (mx - mrun[qb]) * sq[qb] > PF_HEADROOM;
-                    const float alpha = need ? lk_exp2((mrun[qb] - mx) * sq[qb]) : 1.0f;
-                    mrun[qb] = need ? mx : mrun[qb];
+                            for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-                    for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
+                                for (int i = 0; i < 4; ++i) {
+                                    pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -mst[qb]));
+                                    pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -mst[qb]));
+                                }
+                        } else {
+                            const float k = need ? floorf(u + PF_P_BIAS) : 0.0f;      // 0 or 6 .. 19
+                            mst[qb] += k;
+                            const float sc = ldexpf(1.0f, -(int) k);
+                            const _Float16 sh = (_Float16) sc;                         // exact (2^-19: an fp16 subnormal)
+                            const lk_h8 s8 = { sh, sh, sh, sh, sh, sh, sh, sh };
+#pragma unroll
+                            for (int kk = 0; kk < 2; ++kk) pb[qb][kk] *= s8;
+#pragma unroll
+                            for (int db = 0; db < 5; ++db) acc[db][qb] *= sc;
+                        }
+                    }
+                } else {
+                    // (unpaired launches: the running max itself and the p
+                    // formed again; the variant above measured 6% slower on
+                    // C5's deep chunks, where rescales are rare, through the
+                    // register allocation of the common path)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int qb = 2 * hq + j;
+                        const float mx = row_max(j);
+                        // key 0 is visible to every query, so mst is finite after tile 0
+                        const bool need = (mx - mst[qb]) * sq[qb] > PF_HEADROOM;
+                        const float alpha = need ? lk_exp2((mst[qb] - mx) * sq[qb]) : 1.0f;
+                        mst[qb] = need ? mx : mst[qb];
+#pragma unroll
+                        for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
+                    }
+                    make_p();
                 }
-                make_p();
             }
         }
         // ---- O^T += V^T . P^T over the 64 keys, 32 per MFMA -----------------------
@@ -780,7 +847,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 const int row = 16 * qb + col;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) A[(4 * db + g) * PF_BQ + row] = acc[db][qb];
-                if (g == 0) ML[row] = make_float2(fmaf(mrun[qb], sq[qb], PF_P_BIAS), acc[4][qb][0]);
+                if (g == 0) ML[row] = make_float2(moff(qb), acc[4][qb][0]);
             }
             return;
         }
@@ -806,7 +873,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 #pragma unroll
                     for (int qb = 0; qb < PF_QB; ++qb) acc[db][qb] = (lk_f4){ 0.f, 0.f, 0.f, 0.f };
 #pragma unroll
-                for (int qb = 0; qb < PF_QB; ++qb) mrun[qb] = -INFINITY;
+                for (int qb = 0; qb < PF_QB; ++qb) mst[qb] = -INFINITY;
             }
         }
         // ---- group A's part of bj into group B's, through LDS (the tile stages
@@ -822,7 +889,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 const int row = 16 * qb + col;
 #pragma unroll
                 for (int db = 0; db < 4; ++db) A[(4 * db + g) * PF_BQ + row] = acc[db][qb];
-                ML[row] = make_float2(fmaf(mrun[qb], sq[qb], PF_P_BIAS), acc[4][qb][0]);
+                ML[row] = make_float2(moff(qb), acc[4][qb][0]);
             }
         }
         __syncthreads();
@@ -832,7 +899,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             for (int qb = 0; qb < PF_QB; ++qb) {
                 const int row = 16 * qb + col;
                 const float2 ml = ML[row];
-                const float mb = fmaf(mrun[qb], sq[qb], PF_P_BIAS);
+                const float mb = moff(qb);
                 const float mx = fmaxf(mb, ml.x);
                 const float fb = lk_exp2(mb - mx), fa = lk_exp2(ml.x - mx);
 #pragma unroll
