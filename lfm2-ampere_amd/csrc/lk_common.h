@@ -39,6 +39,7 @@ typedef unsigned short lk_u16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned short lk_u16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 lk_h8  __attribute__((ext_vector_type(8)));
 typedef _Float16 lk_h4  __attribute__((ext_vector_type(4)));
+typedef unsigned short lk_u16x4 __attribute__((ext_vector_type(4)));
 typedef float    lk_f4  __attribute__((ext_vector_type(4)));
 typedef int      lk_i4  __attribute__((ext_vector_type(4)));
 

@@ -543,30 +543,31 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // Per query, p = 2^(x*sq - moff) with the exponent offset moff = m*sq +
     // PF_P_BIAS for a running max m (score units), -inf before the first
     // tile.  mst holds m (unpaired launches) or moff itself (PAIR, whose
-    // rescale below moves moff by whole powers of two).
+    // first tile sets moff from the tile max before any p is formed).
     float mst[PF_QB];
 #pragma unroll
     for (int qb = 0; qb < PF_QB; ++qb) mst[qb] = -INFINITY;
     const _Float16 one = (_Float16) 1.0f;
     const lk_h8 ones = { one, one, one, one, one, one, one, one };
-    // The running max is only raised when a score exceeds it by more than
-    // PF_HEADROOM (log2 units), so most tiles skip the rescale.  p is formed
-    // as 2^(sq*(x - m) - PF_P_BIAS) with PF_HEADROOM = PF_P_BIAS + 1: a score
-    // at the headroom limit gives p = 2, the first fp16 value with bit 14 set,
-    // so "some p is past the limit (or inf/NaN)" is one bit of the OR of all p.
-    // p <= 2 keeps fp16 far from overflow.  With the bias 2^-5, p is a normal
-    // fp16 down to 2^-9 of the running max's p and below that keeps an
-    // absolute step of 2^-24 (2^-19 of it).  A larger bias trades accuracy on
-    // long diffuse rows for fewer rescales: at 2^-7 (headroom 8) rows over
+    // p is formed as 2^(sq*(x - m) - PF_P_BIAS): the max m the offset was set
+    // from has p = 2^-5, and p is a normal fp16 down to 2^-9 of that p; below
+    // it keeps an absolute step of 2^-24 (2^-19 of it).  The offset is only
+    // raised once some p reaches 2^PF_P_BIG = 2^15 (fp16 ends at 2^16), i.e.
+    // a score 20 log2 units past the running max: a p above 2^-5 only gains
+    // relative precision, and the P.V and row-sum MFMAs accumulate in fp32.
+    // (Raising it at p >= 2, a headroom of 6, rescaled 8-46% of the query
+    // halves of shallow chunks and cost C4 about 8%.)  The test is two-level:
+    // bit 14 of the OR of all p words (some p >= 2, inf or NaN: the first fp16
+    // value with bit 14 set is 2), then, only then, the max of the words.
+    // A larger bias costs accuracy on long diffuse rows: at 2^-7, rows over
     // 8000 keys measured 8e-4 relative error against float64, at 2^-5 about
-    // 1e-4 to 2.6e-4 (as the unbiased form), with C5 unchanged and the 4096-key
-    // chunk 3% slower.  The bias cancels in o = acc / l; partial records carry
-    // it in their max.
+    // 1e-4 to 2.6e-4 (as the unbiased form).  The bias cancels in
+    // o = acc / l; partial records carry it in their max.
 #ifndef PF_PBIAS
 #define PF_PBIAS 5
 #endif
     constexpr float PF_P_BIAS = (float) PF_PBIAS;
-    constexpr float PF_HEADROOM = PF_P_BIAS + 1.0f;
+    constexpr float PF_P_BIG = 15.0f;
     auto moff = [&](int qb) -> float { return PAIR ? mst[qb] : fmaf(mst[qb], sq[qb], PF_P_BIAS); };
 
     // ---- per-lane LDS read offsets: the swizzles above depend only on the lane
@@ -661,9 +662,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             }
             // ---- online softmax, per query (lane column); p = 2^(x*sq - moff)
             // p is formed against the running offset first.  The exact tile max
-            // is only needed when some score passes the headroom (or the max
-            // is still -inf: first tile): that is bit 14 of an fp16 p (p >= 2,
-            // inf or NaN), found in the OR of the p words, with no cross-lane
+            // is only needed when some p reaches 2^PF_P_BIG (or the max is still
+            // -inf: first tile), which is first screened by bit 14 of an fp16 p
+            // (p >= 2, inf or NaN) in the OR of the p words, with no cross-lane
             // reduction.
             auto make_p = [&]() {
 #pragma unroll
@@ -723,68 +724,59 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 #pragma unroll
                 for (int t = 0; t < (n + 2) / 3; ++t)
                     pw[t] = pw[3 * t] | (3 * t + 1 < n ? pw[3 * t + 1] : 0u) | (3 * t + 2 < n ? pw[3 * t + 2] : 0u);
-            if (__ballot(pw[0] & 0x40004000u)) {               // wave-uniform, rare
-                if constexpr (PAIR) {
-                    // Raise the offset of the queries whose max passed the
-                    // headroom (u = max*sq - moff > PF_HEADROOM - PF_P_BIAS) by
-                    // the integer k = floor(u + PF_P_BIAS): their p (fp16, below
-                    // 2^15 while u <= 14) and acc then scale by exactly 2^-k, one
-                    // packed fp16 multiply per two p instead of forming them
-                    // again, and the largest p lands in [2^-PF_P_BIAS,
-                    // 2^(1-PF_P_BIAS)), at least as far from fp16's subnormals
-                    // as p formed against the exact max.  Past u = 14 (a p at
-                    // fp16's limit) the offset becomes max*sq + PF_P_BIAS and
-                    // that query block's p are formed again.  Shallow chunks
-                    // (the paired launches) rescale in 10-45% of the query
-                    // halves, deep ones in about 1.5%.
+            if (__ballot(pw[0] & 0x40004000u)) {               // some p >= 2 (or inf/NaN)
+                // any p >= 2^PF_P_BIG (or inf/NaN)?  The fp16 bit patterns of
+                // p >= 0 order as unsigned integers: a packed u16 max of the
+                // p words against 0x7800.
+                lk_u16x8 pm = __builtin_elementwise_max(__builtin_bit_cast(lk_u16x8, pb[2 * hq][0]),
+                                                        __builtin_bit_cast(lk_u16x8, pb[2 * hq][1]));
+                pm = __builtin_elementwise_max(pm, __builtin_bit_cast(lk_u16x8, pb[2 * hq + 1][0]));
+                pm = __builtin_elementwise_max(pm, __builtin_bit_cast(lk_u16x8, pb[2 * hq + 1][1]));
+                const lk_u16x4 p4 = __builtin_elementwise_max(pm.s0123, pm.s4567);
+                const lk_u16x2 p2 = __builtin_elementwise_max(p4.s01, p4.s23);
+                const unsigned short p1 = p2.x > p2.y ? p2.x : p2.y;
+                if (__ballot(p1 >= 0x7800u)) {                 // wave-uniform, rare
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
                         const int qb = 2 * hq + j;
-                        const float mx = row_max(j);
-                        const float u = fmaf(mx, sq[qb], -mst[qb]);
-                        const bool need = u > PF_HEADROOM - PF_P_BIAS;
-                        if (__ballot(u > 14.0f)) {
-                            const float mn = need ? fmaf(mx, sq[qb], PF_P_BIAS) : mst[qb];
-                            const float alpha = need ? lk_exp2(mst[qb] - mn) : 1.0f;
-                            mst[qb] = mn;
+                        if constexpr (PAIR) {
+                            // the offset of the queries past the limit moves to
+                            // their max + PF_P_BIAS; their p are formed again
+                            const float am = row_max(j) * sq[qb];
+                            const bool need = am - mst[qb] > PF_P_BIG - 1.0f;
+                            if (__ballot(need)) {
+                                const float mn = need ? am + PF_P_BIAS : mst[qb];
+                                const float alpha = need ? lk_exp2(mst[qb] - mn) : 1.0f;
+                                mst[qb] = mn;
+#pragma unroll
+                                for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
+#pragma unroll
+                                for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                                    for (int i = 0; i < 4; ++i) {
+                                        pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -mst[qb]));
+                                        pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -mst[qb]));
+                                    }
+                            }
+                        } else {
+                            // the running max itself; key 0 is visible to every
+                            // query, so mst is finite after tile 0
+                            const float mx = row_max(j);
+                            const bool need = (mx - mst[qb]) * sq[qb] > PF_P_BIG + PF_P_BIAS - 1.0f;
+                            const float alpha = need ? lk_exp2((mst[qb] - mx) * sq[qb]) : 1.0f;
+                            mst[qb] = need ? mx : mst[qb];
 #pragma unroll
                             for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
+                            const float mo = moff(qb);
 #pragma unroll
                             for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
                                 for (int i = 0; i < 4; ++i) {
-                                    pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -mst[qb]));
-                                    pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -mst[qb]));
+                                    pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -mo));
+                                    pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -mo));
                                 }
-                        } else {
-                            const float k = need ? floorf(u + PF_P_BIAS) : 0.0f;      // 0 or 6 .. 19
-                            mst[qb] += k;
-                            const float sc = ldexpf(1.0f, -(int) k);
-                            const _Float16 sh = (_Float16) sc;                         // exact (2^-19: an fp16 subnormal)
-                            const lk_h8 s8 = { sh, sh, sh, sh, sh, sh, sh, sh };
-#pragma unroll
-                            for (int kk = 0; kk < 2; ++kk) pb[qb][kk] *= s8;
-#pragma unroll
-                            for (int db = 0; db < 5; ++db) acc[db][qb] *= sc;
                         }
                     }
-                } else {
-                    // (unpaired launches: the running max itself and the p
-                    // formed again; the variant above measured 6% slower on
-                    // C5's deep chunks, where rescales are rare, through the
-                    // register allocation of the common path)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const int qb = 2 * hq + j;
-                        const float mx = row_max(j);
-                        // key 0 is visible to every query, so mst is finite after tile 0
-                        const bool need = (mx - mst[qb]) * sq[qb] > PF_HEADROOM;
-                        const float alpha = need ? lk_exp2((mst[qb] - mx) * sq[qb]) : 1.0f;
-                        mst[qb] = need ? mx : mst[qb];
-#pragma unroll
-                        for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
-                    }
-                    make_p();
                 }
             }
         }

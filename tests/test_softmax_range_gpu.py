@@ -12,12 +12,17 @@ decode: tests/test_attn.cu:46-74):
   the spike is seen, but not before it);
 * jump  -- one key ~290 log2 units above the rest, so 2^(x - m) overflows fp32
   on the tile that holds it (inf is caught by the overflow test);
-* step  -- the second half of the keys scores 7-9 log2 units above the first,
-  just past the headroom: one rescale per row, after which the earlier keys
-  still carry a visible share of the weight.
+* step  -- the second half of the keys scores 7-9 log2 units above the first:
+  one decode rescale per row, after which the earlier keys still carry a
+  visible share of the weight;
+* step14 / step21 -- the same with +14.4 / +21.6 log2 units: the prefill
+  kernels raise their exponent offset only once some p reaches 2^15 (20 log2
+  units above the offset's max), so step14 runs on with p up to 2^9.4 and
+  step21 rescales just past that limit.
 
-Prefill runs unsplit, auto-split and in parts of 2 tiles (the combine then
-merges parts whose maxima differ by hundreds of log2 units).
+Prefill runs unsplit, auto-split, in parts of 2 tiles (the combine then
+merges parts whose maxima differ by hundreds of log2 units) and as the paired
+launch (two 4-wave groups per workgroup, merged in LDS).
 """
 import numpy as np
 import pytest
@@ -43,16 +48,21 @@ def _prefill_case(kind, m, P, seed):
         K[S // 2, :, 0] = 200.0
     elif kind == "step":
         K[S // 2:, :, 0] += 5.0                                         # +7.2 log2 units
+    elif kind == "step14":
+        K[S // 2:, :, 0] += 10.0                                        # +14.4 log2 units
+    elif kind == "step21":
+        K[S // 2:, :, 0] += 15.0                                        # +21.6 log2 units
     f16 = lambda a: a.astype(np.float16).view(np.uint16).reshape(-1)
     return f16(K), f16(V), f16(Q)
 
 
 CASES = [("ramp", 200, 300, 96), ("spike", 200, 300, 96), ("jump", 200, 300, 96),
-         ("step", 200, 300, 96), ("step", 100, 2000, 0), ("ramp", 130, 0, 1024), ("jump", 64, 1000, 0)]
+         ("step", 200, 300, 96), ("step", 100, 2000, 0), ("ramp", 130, 0, 1024), ("jump", 64, 1000, 0),
+         ("step14", 200, 300, 96), ("step21", 200, 300, 96), ("step21", 300, 0, 1024), ("step14", 256, 1000, 0)]
 
 
 @pytest.mark.parametrize("kind,m,P,near", CASES, ids=[f"{c[0]}_m{c[1]}_P{c[2]}_n{c[3]}" for c in CASES])
-@pytest.mark.parametrize("split", [-1, 0, 2], ids=["unsplit", "auto", "parts2"])
+@pytest.mark.parametrize("split", [-1, 0, 2, "pair"], ids=["unsplit", "auto", "parts2", "paired"])
 def test_prefill_range(lk, oracle, kind, m, P, near, split):
     K, V, Q = _prefill_case(kind, m, P, seed=m + P)
     S = P + m
@@ -69,13 +79,17 @@ def test_prefill_range(lk, oracle, kind, m, P, near, split):
     lk.pf_k8(kc, 0, S, None, ks, k8, ksc)
     o8 = torch.full((m, 2048), float("nan"), device="cuda")
     o16 = torch.full((m, 2048), float("nan"), device="cuda")
-    lk.pf_split_override(split)
+    if split == "pair":
+        lk.pf_pair_override(1)
+    else:
+        lk.pf_split_override(split)
     try:
         lk.pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, near, sink, o8)
         lk.pf_attn(qh, m, P, kc, vc, o16)
         torch.cuda.synchronize()
     finally:
         lk.pf_split_override(0)
+        lk.pf_pair_override(0)
     o8, o16 = host(o8), host(o16)
     assert np.isfinite(o8).all() and np.isfinite(o16).all()
     ref8 = oracle.pf_ref8(host(q8), host(qsc), host(qcs), Q, m, P, host(k8), host(ksc), ks, K, V, near, sink)
