@@ -145,7 +145,7 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     };
     // Wait until tile `it` is resident for the whole workgroup.  When tile it
     // is awaited, this wave has issued tiles up to min(it + D - 1, ntile - 1)
-    // (tile it + D is fetched only after tile it is consumed); its own fetches
+    // (tile it + D is fetched only after tile it is awaited); its own fetches
     // complete in order, so the rows of those later tiles may stay pending.
     // The barrier then covers the other waves' rows.
     auto wait_tile = [&](int it) {
@@ -164,6 +164,16 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     for (int i = 0; i < D; ++i)
         if (i < ntile) fetch(i);
 
+    // This lane's q values (dims 8g+i and 32+8g+i of head 4w + (col & 3)),
+    // loaded before the producer's sin/cos below so that the two latencies
+    // overlap (a barrier follows the table, and loads do not move across it).
+    const int qrow = (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
+    float qlo[8], qhi[8];
+    {
+        const float * qp = (FUSED ? pr.q_src : q) + qrow;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { qlo[i] = qp[i]; qhi[i] = qp[32 + i]; }
+    }
     // Folded producer: the 32 (cos, sin) entries of position seq-1, 4 per wave.
     __shared__ float s_c[FUSED ? LK_HEAD_DIM / 2 : 1], s_s[FUSED ? LK_HEAD_DIM / 2 : 1];
     const int pos = seq - 1;
@@ -208,11 +218,9 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     lk_h8 qbh[2], qbl[2];
     int qsh = 0;                                            // q of this lane's head is scaled by 2^-qsh
     {
-        const int qrow = (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
-        const float * qp = (FUSED ? pr.q_src : q) + qrow;
         float lo[8], hi[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { lo[i] = qp[i]; hi[i] = qp[32 + i]; }
+        for (int i = 0; i < 8; ++i) { lo[i] = qlo[i]; hi[i] = qhi[i]; }
         if constexpr (FUSED) {
             lk_norm_rope_pair8(lo, hi, pr.q_norm, g, s_c, s_s);
             if (sp == 0 && col < 4) {                       // the working q, once
@@ -330,6 +338,10 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
 
     for (int it = 0; it < ntile; ++it) {
         wait_tile(it);
+        // buffer (it + D) % NBUF = (it - 1) % NBUF: every wave finished reading
+        // it before the barrier in wait_tile, so the next DMA goes out before
+        // this tile is consumed (one barrier per tile)
+        if (it + D < ntile) fetch(it + D);
         if (own_pos && it == ntile - 1 && col == 0) {
             // the new row, as the cache now holds it (the tile's copy may predate
             // the store above); wave w alone reads kv head w's bytes of a row
@@ -341,9 +353,6 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
             *(lk_h8 *) (b + (LK_DEC_TILE + rt) * LK_DEC_ROWB + 64) = kv_h[3];
         }
         consume(s_tile[it % LK_DEC_NBUF], it);
-        // every wave is done reading buffer it % NBUF before it is refilled
-        __builtin_amdgcn_s_barrier();
-        if (it + D < ntile) fetch(it + D);
     }
 
     // Partial record of query head 4w + c, written by the lanes of columns
