@@ -326,6 +326,13 @@ int lk_pf_qk_i32(const int8_t * q8, int m, const int8_t * k8, int n,
  * work; no counterpart in the reference (its kernels do not split). */
 int lk_pf_plan_items(int m, int P, int near, int sink, int int8, int32_t * items, int max_items);
 
+/* Test hook: the 32 rotary frequencies theta^(-i/32) (theta = 1e7, reference
+ * kernels.cuh:22-24) the producers use, as fp32, into out[32].  The kernels
+ * keep them as constants rather than forming them with an fp64 pow; this lets
+ * a CPU test check them against the host's pow.  No counterpart in the
+ * reference (its kernels call powf). */
+int lk_rope_freq_table(float * out);
+
 /* Measurement reference, not on the attention path: a plain streaming read of
  * `bytes` (a multiple of 16, 16-byte aligned) at `src`, for the practical HBM
  * read rate next to the decode kernels' (the datasheet peak is not reachable

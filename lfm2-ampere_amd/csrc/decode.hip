@@ -63,8 +63,8 @@ __device__ __forceinline__ void lk_split_h(float x, _Float16 & hi, _Float16 & lo
 // ^32, ^16: lk_xrow_sum adds in that order, both partners the same two
 // values), then 4, 2, 1 in lane; 1/sqrt in fp64 rounded once; the rotation of
 // the pair (d, d+32) with the table entry d.
-__device__ __forceinline__ void lk_norm_rope_pair8(float (&lo)[8], float (&hi)[8], const float * __restrict__ wn,
-                                                   int g, const float * s_c, const float * s_s) {
+__device__ __forceinline__ void lk_norm_rope_pair8(float (&lo)[8], float (&hi)[8], const float (&wlo)[8],
+                                                   const float (&whi)[8], int g, const float * s_c, const float * s_s) {
 #pragma clang fp contract(off)
     float t[8];
 #pragma unroll
@@ -79,7 +79,7 @@ __device__ __forceinline__ void lk_norm_rope_pair8(float (&lo)[8], float (&hi)[8
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int d = 8 * g + i;
-        const float yl = (lo[i] * inv) * wn[d], yh = (hi[i] * inv) * wn[32 + d];
+        const float yl = (lo[i] * inv) * wlo[i], yh = (hi[i] * inv) * whi[i];
         const float c = s_c[d], sn = s_s[d];
         lo[i] = yl * c - yh * sn;
         hi[i] = yl * sn + yh * c;
@@ -104,6 +104,38 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     static_assert(LK_DEC_TILE % 16 == 0 && LK_DEC_NBUF >= 2, "decode tile shape");
     __shared__ __attribute__((aligned(16))) unsigned char s_tile[LK_DEC_NBUF][LK_DEC_TILEB];
 
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave = kv head
+    const int col = lane & 15, g = lane >> 4;
+
+    // Every input other than the cache tiles is loaded first, before the tile
+    // DMA below: vector-memory loads complete in issue order, so a load issued
+    // after the DMAs would wait for them (about 3 us at start-up) before the
+    // producer's work could begin.  This lane's q values (dims 8g+i and
+    // 32+8g+i of head 4w + (col & 3)); with the producer folded in also the
+    // rotary frequency of table entry 4w + lane (lanes 0-3), the q and k norm
+    // weights and the new row's k and v inputs (used by the slice that holds
+    // the position only).
+    const int qrow = (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
+    float qlo[8], qhi[8], qwlo[8], qwhi[8];
+    float klo[8], khi[8], vlo[8], vhi[8], kwlo[8], kwhi[8];
+    float rfreq = 0.0f;
+    {
+        const float * qp = (FUSED ? pr.q_src : q) + qrow;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { qlo[i] = qp[i]; qhi[i] = qp[32 + i]; }
+        if constexpr (FUSED) {
+            rfreq = lk_rope_freq(4 * w + (lane & 3));
+            const float * kp = pr.k_src + w * LK_HEAD_DIM + 8 * g;
+            const float * vp = pr.v_src + w * LK_HEAD_DIM + 8 * g;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                qwlo[i] = pr.q_norm[8 * g + i]; qwhi[i] = pr.q_norm[32 + 8 * g + i];
+                klo[i] = kp[i]; khi[i] = kp[32 + i]; vlo[i] = vp[i]; vhi[i] = vp[32 + i];
+                kwlo[i] = pr.k_norm[8 * g + i]; kwhi[i] = pr.k_norm[32 + 8 * g + i];
+            }
+        }
+    }
     const int seq = *d_pos + 1;
     int ns, chunk;
     lk_attn_slices(seq, ns, chunk);
@@ -123,10 +155,6 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     }
     const int n = t1 - t0;
     const int ntile = (n + LK_DEC_TILE - 1) / LK_DEC_TILE;
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave = kv head
-    const int col = lane & 15, g = lane >> 4;
 
     // ---- fetch: wave w brings rows w, w+8, ... of each tile (K rows first) ----
     const char * kg = (const char *) (kc + (size_t) t0 * LK_KV_ROW) + 16 * lane;
@@ -164,35 +192,23 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     for (int i = 0; i < D; ++i)
         if (i < ntile) fetch(i);
 
-    // This lane's q values (dims 8g+i and 32+8g+i of head 4w + (col & 3)),
-    // loaded before the producer's sin/cos below so that the two latencies
-    // overlap (a barrier follows the table, and loads do not move across it).
-    const int qrow = (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
-    float qlo[8], qhi[8];
-    {
-        const float * qp = (FUSED ? pr.q_src : q) + qrow;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) { qlo[i] = qp[i]; qhi[i] = qp[32 + i]; }
-    }
     // Folded producer: the 32 (cos, sin) entries of position seq-1, 4 per wave.
     __shared__ float s_c[FUSED ? LK_HEAD_DIM / 2 : 1], s_s[FUSED ? LK_HEAD_DIM / 2 : 1];
     const int pos = seq - 1;
     const bool own_pos = FUSED && t1 == seq;               // this slice holds position pos
     lk_h8 kv_h[4];                                         // its K lo, K hi, V lo, V hi (fp16)
     if constexpr (FUSED) {
-        if (lane < 4) lk_rope_entry(pos, 4 * w + lane, s_c[4 * w + lane], s_s[4 * w + lane]);
+        if (lane < 4) lk_rope_angle(pos, rfreq, s_c[4 * w + lane], s_s[4 * w + lane]);
         __syncthreads();
         if (own_pos) {
             float lo[8], hi[8];
-            const float * kp = pr.k_src + w * LK_HEAD_DIM + 8 * g;
-            const float * vp = pr.v_src + w * LK_HEAD_DIM + 8 * g;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) { lo[i] = kp[i]; hi[i] = kp[32 + i]; }
-            lk_norm_rope_pair8(lo, hi, pr.k_norm, g, s_c, s_s);
+            for (int i = 0; i < 8; ++i) { lo[i] = klo[i]; hi[i] = khi[i]; }
+            lk_norm_rope_pair8(lo, hi, kwlo, kwhi, g, s_c, s_s);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 kv_h[0][i] = (_Float16) lo[i]; kv_h[1][i] = (_Float16) hi[i];
-                kv_h[2][i] = (_Float16) vp[i]; kv_h[3][i] = (_Float16) vp[32 + i];
+                kv_h[2][i] = (_Float16) vlo[i]; kv_h[3][i] = (_Float16) vhi[i];
             }
             if (col == 0) {
                 const size_t off = ((size_t) pos * LK_N_KV_HEADS + w) * LK_HEAD_DIM + 8 * g;
@@ -222,7 +238,7 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
 #pragma unroll
         for (int i = 0; i < 8; ++i) { lo[i] = qlo[i]; hi[i] = qhi[i]; }
         if constexpr (FUSED) {
-            lk_norm_rope_pair8(lo, hi, pr.q_norm, g, s_c, s_s);
+            lk_norm_rope_pair8(lo, hi, qwlo, qwhi, g, s_c, s_s);
             if (sp == 0 && col < 4) {                       // the working q, once
                 float * qo = pr.q_out + qrow;
                 *(lk_f4 *) qo        = (lk_f4){ lo[0], lo[1], lo[2], lo[3] };

@@ -186,11 +186,35 @@ __host__ __device__ __forceinline__ void lk_attn_slices(int seq, int & ns, int &
 // ---- rotary embedding constants and table entry (qknr.hip, decode.hip) -----------
 // Reference kernels.cuh:22-24: LK_EPS 1e-5, LK_ROPE_THETA 1e7.  Entry i < 32 of
 // position pos: f = theta^(-i/32) and the cosine and sine of the fp32 angle
-// (float) pos * f, each evaluated in fp64 and rounded once to fp32.
+// (float) pos * f, each evaluated in fp64 and rounded once to fp32.  The 32
+// frequencies are constants: (float) pow(1e7, -i / 32.0) in fp64, rounded once
+// (a test checks them against the host's pow, the oracle's formula); forming
+// them on the device with pow costs a chain of about 220 dependent fp64
+// instructions.
 #define LK_EPS_F        1e-5f
 #define LK_ROPE_THETA_D 10000000.0
+#define LK_ROPE_FREQ_INIT \
+    0x1p+0f, 0x1.356656p-1f, 0x1.75f034p-2f, 0x1.c3f06cp-3f, \
+    0x1.111aeep-3f, 0x1.4a12aep-4f, 0x1.8eec7ep-5f, 0x1.e222ecp-6f, \
+    0x1.235a72p-6f, 0x1.6020a4p-7f, 0x1.a99428p-8f, 0x1.012cfap-8f, \
+    0x1.36d21ap-9f, 0x1.77a7d8p-10f, 0x1.c603c4p-11f, 0x1.125c04p-11f, \
+    0x1.4b96bep-12f, 0x1.90c182p-13f, 0x1.e459c6p-14f, 0x1.24b0fep-14f, \
+    0x1.61bea2p-15f, 0x1.ab8884p-16f, 0x1.025b58p-16f, 0x1.383f88p-17f, \
+    0x1.796182p-18f, 0x1.c8198cp-19f, 0x1.139e96p-19f, 0x1.4d1c98p-20f, \
+    0x1.9298acp-21f, 0x1.e69338p-22f, 0x1.26091cp-22f, 0x1.635e88p-23f
+// Entry i (0..31) by a select tree over the bits of i on immediate constants:
+// no memory access (a load of a constant table went to L2 or HBM at the start
+// of every producer workgroup and cost more than the fp64 pow it replaced).
 __device__ __forceinline__ float lk_rope_freq(int i) {
-    return (float) pow(LK_ROPE_THETA_D, -(double) i / 32.0);
+    constexpr float T[LK_HEAD_DIM / 2] = { LK_ROPE_FREQ_INIT };
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = (i & 1) ? T[2 * k + 1] : T[2 * k];
+#pragma unroll
+    for (int b = 1, n = 8; n >= 1; ++b, n >>= 1)
+#pragma unroll
+        for (int k = 0; k < n; ++k) v[k] = ((i >> b) & 1) ? v[2 * k + 1] : v[2 * k];
+    return v[0];
 }
 __device__ __forceinline__ void lk_rope_angle(int pos, float f, float & c, float & s) {
     const float a = (float) pos * f;                           // fp32 product, as the reference
@@ -198,9 +222,6 @@ __device__ __forceinline__ void lk_rope_angle(int pos, float f, float & c, float
     sincos((double) a, &sd, &cd);
     c = (float) cd;
     s = (float) sd;
-}
-__device__ __forceinline__ void lk_rope_entry(int pos, int i, float & c, float & s) {
-    lk_rope_angle(pos, lk_rope_freq(i), c, s);
 }
 
 // ---- int8 row quantiser on 8-lane groups (shared by prefill.hip, qknr.hip) -----

@@ -3,6 +3,7 @@
 #include "lk_common.h"
 #include <cstdarg>
 #include <cstdio>
+#include <cstring>
 
 static thread_local char g_lk_err[512] = "no error";
 
@@ -31,4 +32,11 @@ extern "C" int lk_attn_config(int * split_cap, int * target_n, int * split_min) 
 
 extern "C" size_t lk_attn_part_bytes(void) {
     return (size_t) LK_N_HEADS * LK_ATTN_SPLIT * LK_ATTN_PARTW * sizeof(float);
+}
+
+extern "C" int lk_rope_freq_table(float * out) {
+    static const float tab[LK_HEAD_DIM / 2] = { LK_ROPE_FREQ_INIT };
+    if (!out) return lk_fail(hipErrorInvalidValue, "lk_rope_freq_table: null pointer");
+    memcpy(out, tab, sizeof tab);
+    return 0;
 }

@@ -35,15 +35,20 @@
 #define LK_QKNR_ROWS    (LK_N_HEADS + LK_N_KV_HEADS)   // 40 groups per token
 #define LK_QKNR_THREADS (LK_QKNR_ROWS * 8)              // 320
 
+// The rotary frequency of table entry threadIdx.x (threads 0..31; others get
+// entry 0, unused), to be loaded before anything else the table waits for.
+__device__ __forceinline__ float lk_rope_freq_lane() {
+    return lk_rope_freq(threadIdx.x < LK_HEAD_DIM / 2 ? (int) threadIdx.x : 0);
+}
 // (cos, sin) of the 32 rotary angles of position pos, into LDS (threads 0..31).
-__device__ __forceinline__ void lk_rope_table(int pos, float * s_c, float * s_s) {
+__device__ __forceinline__ void lk_rope_table(int pos, float f, float * s_c, float * s_s) {
     const int i = threadIdx.x;
-    if (i < LK_HEAD_DIM / 2) lk_rope_entry(pos, i, s_c[i], s_s[i]);
+    if (i < LK_HEAD_DIM / 2) lk_rope_angle(pos, f, s_c[i], s_s[i]);
 }
 
 // Norm + rotation of one 64-wide row held by an 8-lane group (lane j: values
 // 8j .. 8j+7).  v in, out (rotated, fp32) out.
-__device__ __forceinline__ void lk_norm_rope8(const float (&v)[8], const float * __restrict__ w,
+__device__ __forceinline__ void lk_norm_rope8(const float (&v)[8], const float (&w)[8],
                                               const float * s_c, const float * s_s, int j,
                                               float (&out)[8]) {
 #pragma clang fp contract(off)
@@ -63,7 +68,7 @@ __device__ __forceinline__ void lk_norm_rope8(const float (&v)[8], const float *
     const float inv = (float) (1.0 / sqrt((double) arg));
     float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = (v[i] * inv) * w[8 * j + i];
+    for (int i = 0; i < 8; ++i) y[i] = (v[i] * inv) * w[i];
     const bool lo = j < 4;                                     // values d < 32
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -96,24 +101,27 @@ lk_k_qk_norm_rope(const float * qs, const float * ks, float * qf, float * kf, co
                   const float * __restrict__ qn, const float * __restrict__ kn,
                   const int * __restrict__ d_pos, _Float16 * __restrict__ kc, _Float16 * __restrict__ vc) {
     __shared__ float s_c[LK_HEAD_DIM / 2], s_s[LK_HEAD_DIM / 2];
-    const int pos = *d_pos;
-    lk_rope_table(pos, s_c, s_s);
-    __syncthreads();
+    // every load goes out before the table's barrier (loads do not move across it)
+    const float rf = lk_rope_freq_lane();
     const int g = threadIdx.x >> 3, j = threadIdx.x & 7;
     const bool isq = g < LK_N_HEADS;
     const int h = isq ? g : g - LK_N_HEADS;
     const float * src = isq ? qs + h * LK_HEAD_DIM : ks + h * LK_HEAD_DIM;
     float * row = isq ? qf + h * LK_HEAD_DIM : kf + h * LK_HEAD_DIM;
-    float v[8], out[8];
+    float v[8], out[8], vv[8];
+    float wn[8];                                                  // norm weights of values 8j..8j+7
     lk_load8f(src + 8 * j, v);
-    lk_norm_rope8(v, isq ? qn : kn, s_c, s_s, j, out);
+    lk_load8f(vf + (isq ? 0 : h * LK_HEAD_DIM) + 8 * j, vv);      // V row (k groups)
+    lk_load8f((isq ? qn : kn) + 8 * j, wn);
+    const int pos = *d_pos;
+    lk_rope_table(pos, rf, s_c, s_s);
+    __syncthreads();
+    lk_norm_rope8(v, wn, s_c, s_s, j, out);
     *(lk_f4 *) (row + 8 * j)     = (lk_f4){ out[0], out[1], out[2], out[3] };
     *(lk_f4 *) (row + 8 * j + 4) = (lk_f4){ out[4], out[5], out[6], out[7] };
     if (!isq) {
         const size_t off = ((size_t) pos * LK_N_KV_HEADS + h) * LK_HEAD_DIM + 8 * j;
         lk_store8h(kc + off, out, 1.0f);
-        float vv[8];
-        lk_load8f(vf + h * LK_HEAD_DIM + 8 * j, vv);
         lk_store8h(vc + off, vv, 1.0f);
     }
 }
@@ -129,23 +137,26 @@ lk_k_pf_qknr(const float * __restrict__ Y, const float * __restrict__ qn, const 
 #pragma clang fp contract(off)
     __shared__ float s_c[LK_HEAD_DIM / 2], s_s[LK_HEAD_DIM / 2];
     const int t = blockIdx.x, pos = P + t;
-    lk_rope_table(pos, s_c, s_s);
-    __syncthreads();
+    // every load goes out before the table's barrier (loads do not move across it)
+    const float rf = lk_rope_freq_lane();
     const int g = threadIdx.x >> 3, j = threadIdx.x & 7;
     const bool isq = g < LK_N_HEADS;
     const int h = isq ? g : g - LK_N_HEADS;
     const float * y = Y + (size_t) t * 3072;
-    float v[8], out[8];
+    float v[8], out[8], vv[8];
     lk_load8f(y + (isq ? h * LK_HEAD_DIM : 2048 + h * LK_HEAD_DIM) + 8 * j, v);
-    lk_norm_rope8(v, isq ? qn : kn, s_c, s_s, j, out);
+    lk_load8f(y + 2560 + (isq ? 0 : h * LK_HEAD_DIM) + 8 * j, vv);   // V row (k groups)
+    float wn[8];                                                     // norm weights of values 8j..8j+7
+    lk_load8f((isq ? qn : kn) + 8 * j, wn);
+    lk_rope_table(pos, rf, s_c, s_s);
+    __syncthreads();
+    lk_norm_rope8(v, wn, s_c, s_s, j, out);
     if (isq) {
         lk_store8h(qh + (size_t) t * LK_HIDDEN + h * LK_HEAD_DIM + 8 * j, out, 0.125f);
         return;
     }
     const size_t off = ((size_t) pos * LK_N_KV_HEADS + h) * LK_HEAD_DIM + 8 * j;
     lk_store8h(kc + off, out, 1.0f);
-    float vv[8];
-    lk_load8f(y + 2560 + h * LK_HEAD_DIM + 8 * j, vv);
     lk_store8h(vc + off, vv, 1.0f);
     if (k8) {                                                  // wave-uniform
         float kq[8];
@@ -174,6 +185,10 @@ extern "C" int lk_qk_norm_rope(float * qf, float * kf, const float * vf, const f
                                void * stream) {
     if (!qf || !kf || !vf || !qn || !kn || !d_pos || !kc || !vc)
         return lk_fail(hipErrorInvalidValue, "lk_qk_norm_rope: null pointer argument");
+    // the widths the kernel loads and stores at: 16 bytes (8 fp32 in, 8 fp16 out)
+    if (((uintptr_t) qf | (uintptr_t) kf | (uintptr_t) vf | (uintptr_t) qn | (uintptr_t) kn |
+         (uintptr_t) kc | (uintptr_t) vc) & 15)
+        return lk_fail(hipErrorInvalidValue, "lk_qk_norm_rope: qf, kf, vf, qn, kn, kc and vc must be 16-byte aligned");
     return lk_qknr_decode_launch(qf, kf, qf, kf, vf, qn, kn, d_pos, kc, vc, lk_stream(stream));
 }
 
@@ -184,6 +199,11 @@ extern "C" int lk_pf_qknr(const float * Y, const float * qn, const float * kn, i
     if (m == 0) return 0;
     if (!Y || !qn || !kn || !qh || !kc || !vc)
         return lk_fail(hipErrorInvalidValue, "lk_pf_qknr: null pointer argument");
+    // the widths the kernel loads and stores at: Y, qn, kn, qh, kc, vc 16 bytes,
+    // k8 8 bytes, ksc and cm 4 bytes
+    if ((((uintptr_t) Y | (uintptr_t) qn | (uintptr_t) kn | (uintptr_t) qh | (uintptr_t) kc | (uintptr_t) vc) & 15) ||
+        ((uintptr_t) k8 & 7) || (((uintptr_t) ksc | (uintptr_t) cm) & 3))
+        return lk_fail(hipErrorInvalidValue, "lk_pf_qknr: misaligned argument (Y, qn, kn, qh, kc, vc 16 B; k8 8 B; ksc, cm 4 B)");
     if (k8 && (!ksc || kstride % 4 != 0 || kstride < P + m))
         return lk_fail(hipErrorInvalidValue, "lk_pf_qknr: k8 needs ksc and kstride %d (multiple of 4, >= P+m %d)",
                        kstride, P + m);

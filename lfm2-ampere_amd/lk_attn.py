@@ -33,7 +33,7 @@ EXPORTS = (
     "lk_decode_step_graph_create", "lk_decode_graph_run",
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
     "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows", "lk_gemv_q4_0", "lk_pf_gemm_q4_0",
-    "lk_attn_decode_noalloc",
+    "lk_attn_decode_noalloc", "lk_rope_freq_table",
 )
 
 
@@ -62,6 +62,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     sig = {
         "lk_attn_config": ([P, P, P], I),
         "lk_attn_part_bytes": ([], S),
+        "lk_rope_freq_table": ([P], I),
         "lk_last_error": ([], ctypes.c_char_p),
         "lk_attn_split": ([P, P, P, P, P, P], I),
         "lk_attn_combine": ([P, P, P, P, P], I),

@@ -28,6 +28,23 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_rope_frequency_constants_match_host_pow():
+    """The producers' rotary frequencies are compile-time constants; they must be
+    (float) pow(1e7, -i/32) evaluated in fp64 and rounded once, the formula the
+    oracle evaluates with the host's pow (Python's math.pow is the same C pow)."""
+    import math
+    import numpy as np
+    import lk_attn
+    lib = ctypes.CDLL(lk_attn.LIB_PATH)
+    lib.lk_rope_freq_table.argtypes = [ctypes.c_void_p]
+    out = np.zeros(32, dtype=np.float32)
+    assert lib.lk_rope_freq_table(out.ctypes.data_as(ctypes.c_void_p)) == 0
+    want = np.array([math.pow(10000000.0, -i / 32.0) for i in range(32)]).astype(np.float32)
+    assert np.array_equal(out.view(np.uint32), want.view(np.uint32))
+    assert out[0] == 1.0 and np.all(np.diff(out) < 0)
+    assert lib.lk_rope_freq_table(None) != 0
+
+
 def test_config_and_part_size():
     import lk_attn
     c = lk_attn.config()
@@ -59,6 +76,12 @@ def test_host_argument_errors():
     assert lib.lk_pf_qknr(p, p, p, 4, 0, p, p, p, p, None, 8, None, None) == 1        # k8 without ksc
     assert lib.lk_pf_qknr(p, p, p, 4, 0, p, p, p, p, p, 6, None, None) == 1          # kstride % 4
     assert lib.lk_pf_qknr(None, None, None, 0, 0, None, None, None, None, None, 0, None, None) == 0
+    q = ctypes.c_void_p(0x1008)      # 8-byte aligned only: the producers load and store 16 bytes
+    assert lib.lk_qk_norm_rope(p, p, p, q, p, p, p, p, None) == 1
+    assert b"16-byte" in lib.lk_last_error()
+    assert lib.lk_pf_qknr(q, p, p, 4, 0, p, p, p, None, None, 0, None, None) == 1
+    assert b"misaligned" in lib.lk_last_error()
+    assert lib.lk_pf_qknr(p, p, p, 4, 0, p, p, p, ctypes.c_void_p(0x1004), p, 8, None, None) == 1   # k8 8 B
     hc = ctypes.c_void_p()
     assert lib.lk_pf_ctx_create(0, 16, 64, 1, 0, 0, 0, ctypes.byref(hc)) == 1
     assert lib.lk_pf_ctx_create(1, 128, 64, 1, 0, 0, 0, ctypes.byref(hc)) == 1    # max_seq < max_chunk
