@@ -371,8 +371,24 @@ def bench_gemv(lk, nmat=128, iters=256):
     t = timed_reps(one, st, iters)
     us = t["median"] * 1e3
     nbytes = rows * bpr * 18 + bpr * 36 + rows * 8
+    # the same launches captured in one hipGraph (nmat nodes, as a decode step
+    # graph holds them), replayed: per-launch time without the eager launch path
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        for i in range(nmat):
+            f(i)
+    def replay():
+        with torch.cuda.stream(st):
+            graph.replay()
+
+    for _ in range(3):
+        replay()
+    st.synchronize()
+    tg = timed_reps(replay, st, 5)
+    us_graph = tg["median"] * 1e3 / nmat
     return {"rows": rows, "bpr": bpr, "us": us, "GBps": nbytes / (us * 1e-6) / 1e9, "bytes": nbytes,
-            "distinct_weight_matrices": nmat, "spread": spread_us(t)}
+            "distinct_weight_matrices": nmat, "spread": spread_us(t),
+            "us_in_graph": us_graph, "GBps_in_graph": nbytes / (us_graph * 1e-6) / 1e9}
 
 
 def bench_pf_gemm(lk, ntok=4096, N=2048, bpr=64, iters=20):
