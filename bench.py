@@ -201,23 +201,30 @@ def bench_prefill_c4(lk, lkc, iters, reps=11):
     torch.cuda.synchronize()
     q_t = timed_reps(lambda: lk.pf_q8(qh, m, None, q8, qsc, qcs, stream=st), st, iters)
     k_t = timed_reps(lambda: lk.pf_k8(kc, 0, S, None, ks, k8, ksc, stream=st), st, iters)
-    f8 = lambda: lk.pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
+    # int8 scoring as an engine without smoothing calls it: Q quantised inside
+    # the attention kernel (q8 = NULL; bit-identical to lk_pf_q8 + lk_pf_attn8);
+    # the precomputed-q8 form is timed beside it
+    f8 = lambda: lk.pf_attn8(None, None, None, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
+    f8p = lambda: lk.pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
     f16 = lambda: lk.pf_attn(qh, m, P, kc, vc, o, stream=st)
     # the next GEMM's planar Q8_1: a separate pass over o, or fused (o not written)
     aqs = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
     asc = torch.empty(m, 64, 2, device="cuda")
     fq = lambda: (f8(), lk.pf_quant_rows(o, m, 2048, 64, aqs, asc, stream=st))
-    ff = lambda: lk.pf_attn8_q81(q8, qsc, qcs, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, None, aqs, asc, stream=st)
+    ff = lambda: lk.pf_attn8_q81(None, None, None, qh, m, P, k8, ksc, ks, kc, vc, 1024, 1, None, aqs, asc, stream=st)
+    lk.pf_q8(qh, m, None, q8, qsc, qcs, stream=st)
     for _ in range(iters):                  # warm-up (clocks settle over the first ~100 us)
         f8()
-    # int8 and fp16 kernels alternate repetition by repetition, so that a drift
-    # of the clocks during the run affects both alike
-    t8, t16 = [], []
+    # the int8 and fp16 kernels alternate repetition by repetition, so that a
+    # drift of the clocks during the run affects them alike
+    t8, t16, t8p = [], [], []
     for _ in range(reps):
         t8.append(timed_reps(f8, st, iters, reps=1)["median"])
         t16.append(timed_reps(f16, st, iters, reps=1)["median"])
+        t8p.append(timed_reps(f8p, st, iters, reps=1)["median"])
     t8.sort()
     t16.sort()
+    t8p.sort()
     a8_t = {"median": t8[reps // 2], "min": t8[0], "max": t8[-1], "reps": reps, "iters": iters}
     a16_t = {"median": t16[reps // 2], "min": t16[0], "max": t16[-1], "reps": reps, "iters": iters}
     q_pass_t = timed_reps(fq, st, iters, reps)
@@ -231,6 +238,7 @@ def bench_prefill_c4(lk, lkc, iters, reps=11):
         "attn8_frac_of_mixed_peak": peak_ms / a8_ms, "attn8": spread_us(a8_t),
         "attn_fp16_us": a16_ms * 1e3, "attn_fp16_TOPS": (oi + of) / (a16_ms * 1e-3) / 1e12,
         "attn_fp16_frac_of_mixed_peak": peak_ms / a16_ms, "attn_fp16": spread_us(a16_t),
+        "attn8_q8_precomputed_us": t8p[reps // 2] * 1e3,
         "q8_us": q_t["median"] * 1e3, "k8_us": k_t["median"] * 1e3,
         "attn8_then_quant_rows_us": q_pass_t["median"] * 1e3, "attn8_q81_fused_us": q_fused_t["median"] * 1e3,
         "attn8_q81_fused": spread_us(q_fused_t),
@@ -244,8 +252,8 @@ C5_SAMPLE_ROWS = 6
 def bench_prefill_c5(lk, lkc, reps):
     """C5: a 131072-token prompt in 32 chunks of 4096, the int8 kernel and the
     fp16 kernel (every tile exact) alternating repetition by repetition; per
-    repetition the attention total over the 32 chunks (the quantisers are timed
-    apart).  Also returns the two kernels' outputs on sampled rows of two
+    repetition the attention total over the 32 chunks (Q quantised inside the
+    int8 attention kernel; the int8 K pass of each chunk is timed apart).  Also returns the two kernels' outputs on sampled rows of two
     chunks, which the CPU leg checks against float64 attention."""
     import torch
     import numpy as np
@@ -253,9 +261,6 @@ def bench_prefill_c5(lk, lkc, reps):
     m = 4096
     ks = lk.kstride_for(S)
     st = torch.cuda.Stream()
-    q8 = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
-    qsc = torch.empty(m, 32, device="cuda")
-    qcs = torch.empty(m, 32, device="cuda")
     k8 = torch.empty(S * 512, dtype=torch.int8, device="cuda")
     ksc = torch.empty(8 * ks + 4, device="cuda")
     o = torch.empty(m, 2048, device="cuda")
@@ -271,10 +276,9 @@ def bench_prefill_c5(lk, lkc, reps):
             a.record(st)
             if int8:
                 lk.pf_k8(kc, P, P + m, None, ks, k8, ksc, stream=st)
-                lk.pf_q8(qchunks[c], m, None, q8, qsc, qcs, stream=st)
             b.record(st)
-            if int8:
-                lk.pf_attn8(q8, qsc, qcs, qchunks[c], m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
+            if int8:        # Q quantised inside the attention kernel (no smoothing)
+                lk.pf_attn8(None, None, None, qchunks[c], m, P, k8, ksc, ks, kc, vc, 1024, 1, o, stream=st)
             else:
                 lk.pf_attn(qchunks[c], m, P, kc, vc, o, stream=st)
             c2.record(st)
@@ -586,16 +590,12 @@ def profile_prefill(lk, lkc, which, launches):
         m, P = 4096, S - 4096
         qc = qh[P:].contiguous()
     ks = lk.kstride_for(P + m)
-    q8 = torch.empty(m, 2048, dtype=torch.int8, device="cuda")
-    qsc = torch.empty(m, 32, device="cuda")
-    qcs = torch.empty(m, 32, device="cuda")
     k8 = torch.empty((P + m) * 512, dtype=torch.int8, device="cuda")
     ksc = torch.empty(8 * ks + 4, device="cuda")
     o = torch.empty(m, 2048, device="cuda")
-    lk.pf_q8(qc, m, None, q8, qsc, qcs)
     lk.pf_k8(kc, 0, P + m, None, ks, k8, ksc)
-    for _ in range(launches):
-        lk.pf_attn8(q8, qsc, qcs, qc, m, P, k8, ksc, ks, kc, vc, 1024, 1, o)
+    for _ in range(launches):       # Q quantised inside the kernel, as bench_prefill_c4/c5 time it
+        lk.pf_attn8(None, None, None, qc, m, P, k8, ksc, ks, kc, vc, 1024, 1, o)
     torch.cuda.synchronize()
     oi, of, pairs = pf_ops(m, P)
     log(f"profile: {launches} prefill attention launches ({which}, m {m}, P {P}, "

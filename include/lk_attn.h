@@ -198,7 +198,11 @@ int lk_pf_kmean(const void * kc, int n, float * cm, void * stream);
 /* Replaces k_pf_attn8 (reference prefill.cuh:105-109, prefill.cu:1337-1571).
  * Key tiles of 64 within `near` positions of a 32-query tile's first query,
  * and key tile 0 when `sink` != 0, are scored exactly in fp16; all others use
- * int8 Q.K^T with int32 sums. */
+ * int8 Q.K^T with int32 sums.  q8, qsc and qcs may all be NULL (an extension,
+ * no counterpart in the reference): the kernel then quantises qh itself, with
+ * lk_pf_q8's arithmetic and no smoothing, from the fp16 Q block it stages for
+ * the exact tiles; the output is bit-identical to lk_pf_q8 + this call, and
+ * the separate quantiser pass and its traffic go away. */
 int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * qcs,
                 const void * qh, int m, int P, const int8_t * k8,
                 const float * ksc, int kstride, const void * kc,

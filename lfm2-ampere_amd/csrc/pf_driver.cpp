@@ -9,7 +9,8 @@
 //      smoothing re-derives the mean vector from this chunk's keys first;
 //   3. lk_pf_q8, then lk_pf_attn8 (or lk_pf_attn with int8 scoring off), the
 //      output as fp32 and/or planar Q8_1 (the reference's k_pf_quant_rows
-//      that follows, engine.cu:1126, fused into the attention epilogue).
+//      that follows, engine.cu:1126, fused into the attention epilogue);
+//      without smoothing the attention kernel quantises Q itself (same bits).
 // lk_pf_chunk_done(pos0 + m) after the chunk's last layer moves k8_valid,
 // exactly where the reference does.  Buffers are allocated once, at create.
 #include "lk_common.h"
@@ -97,6 +98,9 @@ extern "C" int lk_pf_chunk_attn(lk_pf_ctx * c, int layer, const float * Y, const
         if (lo < pos0) rc = lk_pf_k8(kc, lo, pos0, cm, c->kstride, k8, ksc, stream);
     }
     if (rc) return rc;
+    if (!cm)   // no smoothing: the attention kernel quantises Q itself (same bits, one pass less)
+        return lk_pf_attn8_q81(nullptr, nullptr, nullptr, c->qh, m, pos0, k8, ksc, c->kstride, kc, vc,
+                               c->near, c->sink, o, aqs, asc, stream);
     rc = lk_pf_q8(c->qh, m, cm, c->q8, c->qsc, c->qcs, stream);
     if (rc) return rc;
     return lk_pf_attn8_q81(c->q8, c->qsc, c->qcs, c->qh, m, pos0, k8, ksc, c->kstride, kc, vc,

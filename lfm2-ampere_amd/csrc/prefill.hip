@@ -478,13 +478,29 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // the first use: one memory round trip for the whole prologue.
     lk_i4 qf8[PF_QB];
     float sq[PF_QB], exa[PF_QB], exb[PF_QB];   // exa, exb: see below
-    auto load_q = [&](bool fill_s_q) {
+    // q8 == nullptr: the int8 Q rows are quantised here from the fp16 block in
+    // LDS (lk_k_pf_q8's arithmetic, without smoothing: q.c = 0) instead of
+    // being loaded; src is the wave's s_q block that holds them.
+    const bool fuse_q = INT8 && q8 == nullptr;
+    auto fill_sq = [&](const lk_h8 (&qv16)[8]) {
+        const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = (lane >> 3) + 8 * i;
+            *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * (lane & 7)) = (qbase + r < m) ? qv16[i] : z8;
+        }
+    };
+    auto load_q = [&](bool fill_s_q, int src) {
         lk_h8 qv16[8];
         if (fill_s_q) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int qr = qbase + (lane >> 3) + 8 * i;
                 qv16[i] = *(const lk_h8 *) (qh + (size_t) (qr < m ? qr : m - 1) * LK_HIDDEN + head * LK_HEAD_DIM + 8 * (lane & 7));
+            }
+            if (fuse_q) {                                 // wave-uniform
+                fill_sq(qv16);
+                __builtin_amdgcn_wave_barrier();          // a wave's LDS accesses complete in order
             }
         }
         // ---- int8 Q operands and per-query scalars (lane column = query) ------
@@ -499,9 +515,38 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             const int qrc = ok ? qr : m - 1;              // clamped: unconditional loads
             const lk_i4 zi = { 0, 0, 0, 0 };
             if (INT8) {
-                const lk_i4 qv = *(const lk_i4 *) (q8 + (size_t) qrc * LK_HIDDEN + head * LK_HEAD_DIM + 16 * qg);
-                const float dv = qsc[(size_t) qrc * LK_N_HEADS + head];
-                const float cv = qcs ? qcs[(size_t) qrc * LK_N_HEADS + head] : 0.0f;
+                lk_i4 qv;
+                float dv, cv;
+                if (fuse_q) {
+#pragma clang fp contract(off)
+                    // values 16qg .. 16qg+15 of row 16qb + qcol (rows past m are zero
+                    // in s_q: am = 0 gives zero quants and d = 0)
+                    const int8_t * rp = s_q[src] + (16 * qb + qcol) * PF_Q_LD + 32 * qg;
+                    const lk_h8 h0 = *(const lk_h8 *) rp, h1 = *(const lk_h8 *) (rp + 16);
+                    float v[16];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) { v[i] = (float) h0[i]; v[8 + i] = (float) h1[i]; }
+                    float am = fabsf(v[0]);
+#pragma unroll
+                    for (int i = 1; i < 16; ++i) am = fmaxf(am, fabsf(v[i]));
+                    am = lk_xrow_max(am);                 // the row's 64 values: lanes ^16, ^32
+                    const float d = am / 127.0f;
+                    const float id = (am > 0.0f) ? 127.0f / am : 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        uint32_t wq = 0;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            wq |= (uint32_t) (uint8_t) (int8_t) (int) __builtin_rintf(v[4 * k + i] * id) << (8 * i);
+                        qv[k] = (int) wq;
+                    }
+                    dv = d * LK_LOG2E_F;
+                    cv = 0.0f;
+                } else {
+                    qv = *(const lk_i4 *) (q8 + (size_t) qrc * LK_HIDDEN + head * LK_HEAD_DIM + 16 * qg);
+                    dv = qsc[(size_t) qrc * LK_N_HEADS + head];
+                    cv = qcs ? qcs[(size_t) qrc * LK_N_HEADS + head] : 0.0f;
+                }
                 qf8[qb] = ok ? qv : zi;
                 const float d = ok ? dv : 0.0f;
                 // scores are kept in units of 1/sq until the exponent (sq > 0
@@ -517,16 +562,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 qf8[qb] = zi; sq[qb] = 1.0f; exa[qb] = LK_LOG2E_F; exb[qb] = 0.0f;
             }
         }
-        if (fill_s_q) {
-            const lk_h8 z8 = { 0, 0, 0, 0, 0, 0, 0, 0 };
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int r = (lane >> 3) + 8 * i;
-                *(lk_h8 *) (s_q[w] + r * PF_Q_LD + 16 * (lane & 7)) = (qbase + r < m) ? qv16[i] : z8;
-            }
-        }
+        if (fill_s_q && !fuse_q) fill_sq(qv16);
     };
-    load_q(true);
+    load_q(true, w);
     // PAIR: every wave's s_q block (group A reads group B's for bj) and the
     // group counters are in place before any group goes on
     if constexpr (PAIR) __syncthreads();
@@ -859,7 +897,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 qt = bj;
                 qbase = bj * PF_BQ;
                 qw = hw + 4;
-                load_q(false);
+                load_q(false, qw);
 #pragma unroll
                 for (int db = 0; db < 5; ++db)
 #pragma unroll
@@ -1345,8 +1383,11 @@ extern "C" int lk_pf_attn8_q81(const int8_t * q8, const float * qsc, const float
     if (m == 0) return 0;
     if (kstride % 4 != 0 || kstride < P + m)
         return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: kstride %d must be a multiple of 4 and >= P+m %d", kstride, P + m);
-    if (!q8 || !qsc || !qh || !k8 || !ksc || !kc || !vc || (!o && !aqs) || (!aqs != !asc))
+    if (!qh || !k8 || !ksc || !kc || !vc || (!o && !aqs) || (!aqs != !asc))
         return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: null pointer argument");
+    // q8 = qsc = qcs = NULL: the kernel quantises qh itself (no smoothing)
+    if (!q8 != !qsc || (!q8 && qcs))
+        return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: q8 and qsc go together; without them (Q quantised in the kernel) qcs must be NULL too");
     return pf_attn_launch<true>(q8, qsc, qcs, (const _Float16 *) qh, m, P, k8, ksc, kstride,
                                 (const _Float16 *) kc, (const _Float16 *) vc, near, sink, o,
                                 aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn8");

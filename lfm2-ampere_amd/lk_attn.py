@@ -288,6 +288,9 @@ def pf_kmean(kc, n, cm, stream=None) -> None:
 
 
 def pf_attn8(q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, stream=None) -> None:
+    """Int8-scored prefill attention (reference k_pf_attn8).  q8, qsc and qcs
+    None: the kernel quantises qh itself (lk_pf_q8's arithmetic, no
+    smoothing), with the same output as the two-kernel path."""
     _check(load().lk_pf_attn8(_ptr(q8), _ptr(qsc), _ptr(qcs), _ptr(qh), m, P, _ptr(k8), _ptr(ksc),
                               kstride, _ptr(kc), _ptr(vc), near, sink, _ptr(o), _stream(stream)),
            "lk_pf_attn8")

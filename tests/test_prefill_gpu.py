@@ -451,6 +451,56 @@ def test_attn_fused_q81_equals_quant_rows(lk, oracle, m, P, near, L, int8):
     assert np.array_equal(host(aqs), qso) and np.array_equal(host(asc).view(np.uint32), sco.view(np.uint32))
 
 
+# ---- Q quantised inside the attention kernel (q8 = qsc = qcs = NULL) ------------------------------
+INQ_CASES = [(4096, 0, 1024, 0), (300, 700, 96, -1), (300, 0, 96, 2), (129, 2000, 1024, 0),
+             (200, 333, 0, 0), (64, 0, 1024, 0), (513, 64, 1024, 0), (1, 77, 96, 0)]
+
+
+@pytest.mark.parametrize("m,P,near,L", INQ_CASES, ids=[f"m{c[0]}_P{c[1]}_n{c[2]}_L{c[3]}" for c in INQ_CASES])
+@pytest.mark.parametrize("pair", [0, -1, 1], ids=["auto", "unpaired", "paired"])
+def test_attn8_in_kernel_q8_is_bit_identical(lk, oracle, m, P, near, L, pair):
+    """lk_pf_attn8 with q8/qsc/qcs NULL quantises Q from the fp16 block it
+    stages anyway (lk_pf_q8's arithmetic, no smoothing): outputs and the fused
+    Q8_1 planes equal the two-kernel path's bit for bit, whatever the launch
+    form (paired, unpaired, split)."""
+    K, V, Q = _inputs(oracle, m, P, 1.0, True)
+    sink = int(near > 0)
+    note(f"pf attn8 in-kernel q8 m={m} P={P} near={near} split={L} pair={pair}")
+    d = _Dev(lk, K, V, Q, m, P, False)
+    outs = []
+    try:
+        lk.pf_split_override(L)
+        lk.pf_pair_override(pair)
+        for q8, qsc in ((d.q8, d.qsc), (None, None)):
+            o = torch.full((m, 2048), float("nan"), device="cuda")
+            aqs = torch.zeros(m, 2048, dtype=torch.int8, device="cuda")
+            asc = torch.zeros(m, 64, 2, device="cuda")
+            lk.pf_attn8(q8, qsc, None if q8 is None else d.qcs, d.qh, m, P, d.k8, d.ksc, d.kstride,
+                        d.kc, d.vc, near, sink, o)
+            lk.pf_attn8_q81(q8, qsc, None if q8 is None else d.qcs, d.qh, m, P, d.k8, d.ksc, d.kstride,
+                            d.kc, d.vc, near, sink, None, aqs, asc)
+            torch.cuda.synchronize()
+            outs.append((host(o), host(aqs), host(asc)))
+    finally:
+        lk.pf_split_override(0)
+        lk.pf_pair_override(0)
+    (o1, a1, s1), (o2, a2, s2) = outs
+    assert np.isfinite(o2).all()
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+    assert np.array_equal(a1, a2) and np.array_equal(s1.view(np.uint32), s2.view(np.uint32))
+
+
+def test_attn8_in_kernel_q8_argument_rules(lk):
+    """q8 and qsc go together; without them qcs (smoothing) must be NULL."""
+    import ctypes
+    lib = lk.load()
+    p = ctypes.c_void_p(0x1000)
+    assert lib.lk_pf_attn8(None, p, None, p, 4, 0, p, p, 4, p, p, 0, 0, p, None) == 1
+    assert lib.lk_pf_attn8(p, None, None, p, 4, 0, p, p, 4, p, p, 0, 0, p, None) == 1
+    assert lib.lk_pf_attn8(None, None, p, p, 4, 0, p, p, 4, p, p, 0, 0, p, None) == 1
+    assert b"qcs" in lib.lk_last_error()
+
+
 # ---- the shared split-K partial buffer: one stream at a time ----------------------------------
 def test_split_scratch_refuses_a_second_stream_while_pending(lk, oracle):
     """Split launches share the library's partial buffer on a device.  A split
