@@ -108,32 +108,31 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave = kv head
     const int col = lane & 15, g = lane >> 4;
 
-    // Every input other than the cache tiles is loaded first, before the tile
-    // DMA below: vector-memory loads complete in issue order, so a load issued
-    // after the DMAs would wait for them (about 3 us at start-up) before the
-    // producer's work could begin.  This lane's q values (dims 8g+i and
-    // 32+8g+i of head 4w + (col & 3)); with the producer folded in also the
-    // rotary frequency of table entry 4w + lane (lanes 0-3), the q and k norm
-    // weights and the new row's k and v inputs (used by the slice that holds
-    // the position only).
+    // The inputs other than the cache tiles are loaded before the tile DMA
+    // below: vector-memory loads complete in issue order, so a load issued
+    // after the DMAs would wait for them (about 3 us at start-up).  This
+    // lane's q values (dims 8g+i and 32+8g+i of head 4w + (col & 3)); with the
+    // producer folded in also the rotary frequency of table entry 4w + lane
+    // (lanes 0-3, a scalar load), the q norm weights and, after the slice
+    // plan, the new row's k and v and the k norm weights (used only by the
+    // workgroup whose slice holds the position).
+    // Loaded untracked (lk_ld16_untracked) and awaited after the DMA issue
+    // with a count that leaves the tile DMAs in flight: a tracked load here
+    // would make the compiler wait for every tile in flight before the
+    // first tile is consumed.  Vector r of each set holds values 4r..4r+3 of
+    // the lane's 16 (8 "lo" at dims 8g.., 8 "hi" at dims 32+8g..).
     const int qrow = (w * LK_G + (col & 3)) * LK_HEAD_DIM + 8 * g;
-    float qlo[8], qhi[8], qwlo[8], qwhi[8];
-    float klo[8], khi[8], vlo[8], vhi[8], kwlo[8], kwhi[8];
+    lk_f4 qv[4], qwv[4], kv4[4], vv4[4], kwv[4];
     float rfreq = 0.0f;
     {
         const float * qp = (FUSED ? pr.q_src : q) + qrow;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) { qlo[i] = qp[i]; qhi[i] = qp[32 + i]; }
+        qv[0] = lk_ld16_untracked(qp);      qv[1] = lk_ld16_untracked(qp + 4);
+        qv[2] = lk_ld16_untracked(qp + 32); qv[3] = lk_ld16_untracked(qp + 36);
         if constexpr (FUSED) {
-            rfreq = lk_rope_freq(4 * w + (lane & 3));
-            const float * kp = pr.k_src + w * LK_HEAD_DIM + 8 * g;
-            const float * vp = pr.v_src + w * LK_HEAD_DIM + 8 * g;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                qwlo[i] = pr.q_norm[8 * g + i]; qwhi[i] = pr.q_norm[32 + 8 * g + i];
-                klo[i] = kp[i]; khi[i] = kp[32 + i]; vlo[i] = vp[i]; vhi[i] = vp[32 + i];
-                kwlo[i] = pr.k_norm[8 * g + i]; kwhi[i] = pr.k_norm[32 + 8 * g + i];
-            }
+            rfreq = lk_rope_freq_quad(w, lane);
+            const float * np = pr.q_norm + 8 * g;
+            qwv[0] = lk_ld16_untracked(np);      qwv[1] = lk_ld16_untracked(np + 4);
+            qwv[2] = lk_ld16_untracked(np + 32); qwv[3] = lk_ld16_untracked(np + 36);
         }
     }
     const int seq = *d_pos + 1;
@@ -155,6 +154,20 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     }
     const int n = t1 - t0;
     const int ntile = (n + LK_DEC_TILE - 1) / LK_DEC_TILE;
+    const int pos = seq - 1;
+    const bool own_pos = FUSED && t1 == seq;               // this slice holds position pos
+    if constexpr (FUSED) {          // loaded by every workgroup: see the wait below
+        const float * kp = pr.k_src + w * LK_HEAD_DIM + 8 * g;
+        const float * vp = pr.v_src + w * LK_HEAD_DIM + 8 * g;
+        const float * np = pr.k_norm + 8 * g;
+        const int off[4] = { 0, 4, 32, 36 };
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            kv4[r] = lk_ld16_untracked(kp + off[r]);
+            vv4[r] = lk_ld16_untracked(vp + off[r]);
+            kwv[r] = lk_ld16_untracked(np + off[r]);
+        }
+    }
 
     // ---- fetch: wave w brings rows w, w+8, ... of each tile (K rows first) ----
     const char * kg = (const char *) (kc + (size_t) t0 * LK_KV_ROW) + 16 * lane;
@@ -187,15 +200,36 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     };
     static_assert(D - 1 <= 4 && 4 * RPW <= 63, "wait_tile handles at most four later tiles in flight");
 
-    // issue the first D tiles before anything else, so HBM starts streaming at once
+    // Issue the first D tiles before anything else, so HBM starts streaming at
+    // once.  All D are issued even for a slice of fewer tiles (the rows past
+    // the slice are clamped to its first row and land in buffers no tile of
+    // the slice uses), so that exactly D*RPW DMAs follow the early loads in
+    // every workgroup and one wait with that count covers those loads.  The
+    // early loads and the wait are unconditional too: the compiler does not
+    // know an untracked load's registers are pending, and around a branch it
+    // may copy them before the wait; lk_wait_vm_tie's operands pin every use
+    // after it only in straight-line code.
 #pragma unroll
-    for (int i = 0; i < D; ++i)
-        if (i < ntile) fetch(i);
+    for (int i = 0; i < D; ++i) fetch(i);
+    lk_wait_vm_tie<D * RPW>(qv);
+    if constexpr (FUSED) {
+        lk_wait_vm_tie<D * RPW>(qwv);
+        lk_wait_vm_tie<D * RPW>(kv4); lk_wait_vm_tie<D * RPW>(vv4); lk_wait_vm_tie<D * RPW>(kwv);
+    }
+    float qlo[8], qhi[8], qwlo[8], qwhi[8];
+    float klo[8], khi[8], vlo[8], vhi[8], kwlo[8], kwhi[8];
+    auto unpack = [](const lk_f4 (&x)[4], float (&lo)[8], float (&hi)[8]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { lo[i] = x[0][i]; lo[4 + i] = x[1][i]; hi[i] = x[2][i]; hi[4 + i] = x[3][i]; }
+    };
+    unpack(qv, qlo, qhi);
+    if constexpr (FUSED) {
+        unpack(qwv, qwlo, qwhi);
+        unpack(kv4, klo, khi); unpack(vv4, vlo, vhi); unpack(kwv, kwlo, kwhi);
+    }
 
     // Folded producer: the 32 (cos, sin) entries of position seq-1, 4 per wave.
     __shared__ float s_c[FUSED ? LK_HEAD_DIM / 2 : 1], s_s[FUSED ? LK_HEAD_DIM / 2 : 1];
-    const int pos = seq - 1;
-    const bool own_pos = FUSED && t1 == seq;               // this slice holds position pos
     lk_h8 kv_h[4];                                         // its K lo, K hi, V lo, V hi (fp16)
     if constexpr (FUSED) {
         if (lane < 4) lk_rope_angle(pos, rfreq, s_c[4 * w + lane], s_s[4 * w + lane]);

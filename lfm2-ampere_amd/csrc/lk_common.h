@@ -216,6 +216,16 @@ __device__ __forceinline__ float lk_rope_freq(int i) {
         for (int k = 0; k < n; ++k) v[k] = ((i >> b) & 1) ? v[2 * k + 1] : v[2 * k];
     return v[0];
 }
+// The same constants in constant memory, for a kernel whose index is
+// wave-uniform: the four entries 4j..4j+3 come in by one scalar load
+// (counted by lgkmcnt, so it never waits behind vector-memory DMA in flight,
+// as a vector load of the table would), and lane l takes entry 4j + (l & 3).
+static __constant__ float lk_rope_tab[LK_HEAD_DIM / 2] = { LK_ROPE_FREQ_INIT };
+__device__ __forceinline__ float lk_rope_freq_quad(int j_uniform, int lane) {
+    const float4 f = *(const float4 *) (lk_rope_tab + 4 * j_uniform);
+    const float lo = (lane & 1) ? f.y : f.x, hi = (lane & 1) ? f.w : f.z;
+    return (lane & 2) ? hi : lo;
+}
 __device__ __forceinline__ void lk_rope_angle(int pos, float f, float & c, float & s) {
     const float a = (float) pos * f;                           // fp32 product, as the reference
     double sd, cd;
@@ -290,6 +300,21 @@ template <int N>
 __device__ __forceinline__ void lk_wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+// A 16-byte global load the compiler does not track (inline asm), for loads
+// issued ahead of the tile DMA (also inline asm, so untracked too): the
+// compiler would otherwise wait for them with vmcnt(0), i.e. for every DMA
+// issued after them.  Their completion is awaited with lk_wait_vm_tie, which
+// takes the loaded registers as operands, so no use can move above it.
+__device__ __forceinline__ lk_f4 lk_ld16_untracked(const void * p) {
+    lk_f4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+template <int N>
+__device__ __forceinline__ void lk_wait_vm_tie(lk_f4 (&a)[4]) {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]) : "n"(N));
 }
 
 // ---- host-side error plumbing (lk_host.cpp) -----------------------------------
