@@ -232,6 +232,30 @@ __device__ __forceinline__ float2 lk_q81_scales(float d, float sum) {
 __device__ __forceinline__ int8_t lk_q81_q(float x, float am, float d) {
     return (am == 0.0f) ? (int8_t) 0 : (int8_t) roundf(x / d);
 }
+// The same q for the many values of one block with one division per block:
+// with r = RN(1/d'), q0 = RN(x*r) is within an ulp of x/d' and
+// RN(q0 + RN(x - q0*d')*r) (two fmas, the remainder exact) is RN(x/d')
+// (Markstein's correction theorem), so roundf sees the bits of x / d.  The
+// theorem needs x/d' and 1/d' in the normal range: blocks with am < 2^-64
+// scale x and d by 2^64 (exact, the quotient unchanged); quotients that are
+// subnormal may differ, but roundf gives 0 for both.  am = 0 (all x = 0)
+// divides by 1.  Checked against x / d on 4e8 (x, am) pairs over am in
+// [2^-140, 2^100], ties and quotients next to .5 included.
+struct LkQ81Div { float s, d, r; };
+__device__ __forceinline__ LkQ81Div lk_q81_div(float am, float d) {
+    LkQ81Div q;
+    q.s = am < 0x1p-64f ? 0x1p64f : 1.0f;
+    q.d = am == 0.0f ? 1.0f : d * q.s;
+    q.r = 1.0f / q.d;
+    return q;
+}
+__device__ __forceinline__ int8_t lk_q81_qd(const LkQ81Div & q, float x) {
+#pragma clang fp contract(off)
+    const float xs = x * q.s;
+    const float q0 = xs * q.r;
+    const float e = __builtin_fmaf(-q0, q.d, xs);
+    return (int8_t) roundf(__builtin_fmaf(e, q.r, q0));
+}
 // From the attention epilogue's layout: lane (col, g) holds, for its query row,
 // dims 16db + 4g + r of the head (db, r = 0..3): block hb (dims 32hb ..
 // 32hb+31) is db = 2hb, 2hb+1 on the 4 lanes g of the row.  The sum follows
@@ -257,11 +281,12 @@ __device__ __forceinline__ void lk_pf_q81_epilogue(const lk_f4 (&a)[4], bool sto
         for (int r = 0; r < 4; ++r) t[r] += __shfl_xor(t[r], 16, 64);
         const float sum = (t[0] + t[2]) + (t[1] + t[3]);
         const float d = am / 127.0f;
+        const LkQ81Div qd = lk_q81_div(am, d);
         uint32_t w0 = 0, w1 = 0;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            w0 |= (uint32_t) (uint8_t) lk_q81_q(x0[r], am, d) << (8 * r);
-            w1 |= (uint32_t) (uint8_t) lk_q81_q(x1[r], am, d) << (8 * r);
+            w0 |= (uint32_t) (uint8_t) lk_q81_qd(qd, x0[r]) << (8 * r);
+            w1 |= (uint32_t) (uint8_t) lk_q81_qd(qd, x1[r]) << (8 * r);
         }
         if (store) {
             *(uint32_t *) (qs + 32 * hb + 4 * g)      = w0;
@@ -281,7 +306,7 @@ __device__ __forceinline__ void lk_pf_q81_epilogue(const lk_f4 (&a)[4], bool sto
 // barriers of their own (a counter in LDS), not at the workgroup barrier, so
 // the two waves of a SIMD (one per group) drift into different phases of
 // their tiles, as two unpaired workgroups do.
-template <bool INT8, bool PAIR>
+template <bool INT8, bool PAIR, bool Q81>
 __global__ void __launch_bounds__(PAIR ? 512 : 256, PAIR ? 1 : 2)
 lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
              const float * __restrict__ qcs, const _Float16 * __restrict__ qh, int m, int P,
@@ -854,7 +879,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                     *(float4 *) (o + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM + 16 * db + 4 * g) =
                         make_float4(a[db][0], a[db][1], a[db][2], a[db][3]);
             }
-            if (aqs) lk_pf_q81_epilogue(a, qr < m, aqs + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM,
+            if constexpr (Q81) lk_pf_q81_epilogue(a, qr < m, aqs + (size_t) qr * LK_HIDDEN + head * LK_HEAD_DIM,
                                         asc + (size_t) qr * (LK_HIDDEN / 32) + 2 * head, g);
         }
     };
@@ -1024,12 +1049,13 @@ lk_k_pf_combine(const float * __restrict__ pbuf, int m, int P, const PfWork work
 #pragma unroll
             for (int i = 0; i < st; ++i) t[i] = t[i] + t[i + st];
         const float d = am / 127.0f;
+        const LkQ81Div qd = lk_q81_div(am, d);
         int8_t * q = aqs + (size_t) qr * LK_HIDDEN + col0;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             uint32_t w = 0;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) w |= (uint32_t) (uint8_t) lk_q81_q(x[4 * c + r], am, d) << (8 * r);
+            for (int r = 0; r < 4; ++r) w |= (uint32_t) (uint8_t) lk_q81_qd(qd, x[4 * c + r]) << (8 * r);
             *(uint32_t *) (q + 4 * c) = w;
         }
         asc[(size_t) qr * (LK_HIDDEN / 32) + col0 / 32] = lk_q81_scales(d, t[0]);
@@ -1339,7 +1365,7 @@ static bool pf_use_pair(int m, int P) {
     return g_pf_split_override <= 0 && P <= m && nq >= 64;
 }
 
-template <bool INT8>
+template <bool INT8, bool Q81>
 static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qcs, const _Float16 * qh,
                           int m, int P, const int8_t * k8, const float * ksc, int kstride,
                           const _Float16 * kc, const _Float16 * vc, int near, int sink, float * o,
@@ -1348,14 +1374,14 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
     if (pf_use_pair(m, P)) {
         wk.n_items = 0; wk.n_split = 0;
         const int npairs = ((m + PF_BQ - 1) / PF_BQ + 1) / 2;
-        hipLaunchKernelGGL((lk_k_pf_attn<INT8, true>), dim3(npairs * LK_N_KV_HEADS), dim3(512), 0, st,
+        hipLaunchKernelGGL((lk_k_pf_attn<INT8, true, Q81>), dim3(npairs * LK_N_KV_HEADS), dim3(512), 0, st,
                            q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk,
                            (float *) nullptr);
         return lk_launch_status(what);
     }
     pf_plan(m, P, near, sink, INT8, wk);
     if (wk.n_items == 0) {
-        hipLaunchKernelGGL((lk_k_pf_attn<INT8, false>), dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0, st,
+        hipLaunchKernelGGL((lk_k_pf_attn<INT8, false, Q81>), dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0, st,
                            q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk,
                            (float *) nullptr);
         return lk_launch_status(what);
@@ -1363,7 +1389,7 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
     int err = 0, dev = 0;
     float * pbuf = pf_part_acquire(st, err, dev);
     if (!pbuf) return err;
-    hipLaunchKernelGGL((lk_k_pf_attn<INT8, false>), dim3(wk.n_items * LK_N_KV_HEADS), dim3(256), 0, st,
+    hipLaunchKernelGGL((lk_k_pf_attn<INT8, false, Q81>), dim3(wk.n_items * LK_N_KV_HEADS), dim3(256), 0, st,
                        q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk, pbuf);
     int rc = lk_launch_status(what);
     if (rc) return rc;
@@ -1388,9 +1414,14 @@ extern "C" int lk_pf_attn8_q81(const int8_t * q8, const float * qsc, const float
     // q8 = qsc = qcs = NULL: the kernel quantises qh itself (no smoothing)
     if (!q8 != !qsc || (!q8 && qcs))
         return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: q8 and qsc go together; without them (Q quantised in the kernel) qcs must be NULL too");
-    return pf_attn_launch<true>(q8, qsc, qcs, (const _Float16 *) qh, m, P, k8, ksc, kstride,
-                                (const _Float16 *) kc, (const _Float16 *) vc, near, sink, o,
-                                aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn8");
+    // the Q8_1 epilogue is a template instance of its own, so that the plain
+    // fp32-output kernel is compiled without it
+    auto go = [&](auto launch) {
+        return launch(q8, qsc, qcs, (const _Float16 *) qh, m, P, k8, ksc, kstride,
+                      (const _Float16 *) kc, (const _Float16 *) vc, near, sink, o,
+                      aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn8");
+    };
+    return aqs ? go(pf_attn_launch<true, true>) : go(pf_attn_launch<true, false>);
 }
 
 extern "C" int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * qcs,
@@ -1408,9 +1439,12 @@ extern "C" int lk_pf_attn_q81(const void * qh, int m, int P, const void * kc, co
     if (m == 0) return 0;
     if (!qh || !kc || !vc || (!o && !aqs) || (!aqs != !asc))
         return lk_fail(hipErrorInvalidValue, "lk_pf_attn: null pointer argument");
-    return pf_attn_launch<false>(nullptr, nullptr, nullptr, (const _Float16 *) qh, m, P, nullptr, nullptr, 0,
-                                 (const _Float16 *) kc, (const _Float16 *) vc, 0, 0, o,
-                                 aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn");
+    auto go = [&](auto launch) {
+        return launch(nullptr, nullptr, nullptr, (const _Float16 *) qh, m, P, nullptr, nullptr, 0,
+                      (const _Float16 *) kc, (const _Float16 *) vc, 0, 0, o,
+                      aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn");
+    };
+    return aqs ? go(pf_attn_launch<false, true>) : go(pf_attn_launch<false, false>);
 }
 
 extern "C" int lk_pf_attn(const void * qh, int m, int P, const void * kc, const void * vc,
