@@ -239,8 +239,9 @@ __device__ __forceinline__ int8_t lk_q81_q(float x, float am, float d) {
 // theorem needs x/d' and 1/d' in the normal range: blocks with am < 2^-64
 // scale x and d by 2^64 (exact, the quotient unchanged); quotients that are
 // subnormal may differ, but roundf gives 0 for both.  am = 0 (all x = 0)
-// divides by 1.  Checked against x / d on 4e8 (x, am) pairs over am in
-// [2^-140, 2^100], ties and quotients next to .5 included.
+// divides by 1.  tests/test_q81_division.py runs this arithmetic on the host
+// against x / d over am in [2^-140, 2^100], ties and quotients next to .5
+// included.
 struct LkQ81Div { float s, d, r; };
 __device__ __forceinline__ LkQ81Div lk_q81_div(float am, float d) {
     LkQ81Div q;
