@@ -375,7 +375,8 @@ int lk_gemv_q4_0(const void * qs, const void * d, const lk_block_q8_1 * xq, int 
  *   out : fp32 [ntok][out_ld] (16-byte aligned, out_ld a multiple of 4, >= N);
  *         out[t][r] = (add ? out[t][r] : 0) + scale[t] * sum over blocks
  *   scale: fp32 [ntok] or NULL (1)
- * N must be a multiple of 128 and bpr of 8 (as pf_gemm_dense requires).  Per
+ * N must be a multiple of 128 and bpr of 8 (as pf_gemm_dense requires), and
+ * the activation quants below 4 GiB (ntok * bpr * 32 bytes).  Per
  * (t, r) the blocks are accumulated in order
  * with the reference's fma sequence; the epilogue rounds the product and the
  * sum separately, as the reference's source writes them. */

@@ -129,6 +129,8 @@ def test_host_argument_errors():
     assert lib.lk_pf_gemm_q4_0(p, p, 128, 64, p, q, 4, None, p, 128, 0, None) == 1   # asc: 16 B
     assert b"misaligned" in lib.lk_last_error()
     assert lib.lk_pf_gemm_q4_0(None, None, 128, 64, None, None, 0, None, None, 128, 0, None) == 0  # no tokens
+    assert lib.lk_pf_gemm_q4_0(p, p, 128, 2048, p, p, 65536, None, p, 128, 0, None) == 1  # 4 GiB of activations
+    assert b"4 GiB" in lib.lk_last_error()
 
 
 def test_python_mirror_fails_loudly_without_library(tmp_path):
