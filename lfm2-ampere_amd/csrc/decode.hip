@@ -145,11 +145,12 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     // neutral record (m = -inf, l = 0, acc = 0) of each query head, so every
     // slot the combine reads is valid without it knowing seq.
     if (t0 >= t1) {
-        for (int i = threadIdx.x; i < LK_N_HEADS * (LK_ATTN_PARTW / 4); i += LK_DEC_THREADS) {
-            const int h = i / (LK_ATTN_PARTW / 4), k = i % (LK_ATTN_PARTW / 4);
-            *(lk_f4 *) (part + ((size_t) h * LK_ATTN_SPLIT + sp) * LK_ATTN_PARTW + 4 * k) =
-                (lk_f4){ k == 0 ? -INFINITY : 0.0f, 0.0f, 0.0f, 0.0f };
+        for (int i = threadIdx.x; i < LK_N_HEADS * 16; i += LK_DEC_THREADS) {
+            const int h = i >> 4, k = i & 15;
+            *(lk_f4 *) (part + lk_part_acc(h, k >> 1, sp) + 4 * (k & 1)) = (lk_f4){ 0.0f, 0.0f, 0.0f, 0.0f };
         }
+        if (threadIdx.x < LK_N_HEADS)
+            *(float2 *) (part + lk_part_ml(threadIdx.x, sp)) = make_float2(-INFINITY, 0.0f);
         return;
     }
     const int n = t1 - t0;
@@ -408,10 +409,11 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     // Partial record of query head 4w + c, written by the lanes of columns
     // c = 0..3: O^T rows 16db + 4g + r; the sum of p is in every row of accl.
     if (col < 4) {
-        float * P = part + ((size_t) (w * LK_G + col) * LK_ATTN_SPLIT + sp) * LK_ATTN_PARTW;
+        const int h = w * LK_G + col;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) *(lk_f4 *) (P + 4 + 16 * db + 4 * g) = acc[db];
-        if (g == 0) { P[0] = mrun; P[1] = accl[0]; }
+        for (int db = 0; db < 4; ++db)          // dims 16db + 4g .. +3: chunk 2db + g/2
+            *(lk_f4 *) (part + lk_part_acc(h, 2 * db + (g >> 1), sp) + 4 * (g & 1)) = acc[db];
+        if (g == 0) *(float2 *) (part + lk_part_ml(h, sp)) = make_float2(mrun, accl[0]);
     }
 }
 
@@ -473,17 +475,17 @@ lk_k_attn_combine(const float * __restrict__ part, const int * __restrict__ d_po
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int d0 = 32 * half + 8 * wv;
 
-    // (m, l) as a float2: a 16-byte load whose pad lanes are dead lets the
-    // register allocator reuse them while the load is in flight, which costs a
-    // full vmcnt wait per record
+    // (m, l) as a float2 from its own plane (a 16-byte load with dead lanes let
+    // the register allocator reuse them while the load was in flight)
     float2 ml[J];
     lk_f4 a0[J], a1[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const float * R = part + ((size_t) head * LK_ATTN_SPLIT + lane + 64 * j) * LK_ATTN_PARTW;
-        ml[j] = *(const float2 *) R;                 // m, l (then two pad floats)
-        a0[j] = *(const lk_f4 *) (R + 4 + d0);
-        a1[j] = *(const lk_f4 *) (R + 8 + d0);
+        const int s = lane + 64 * j;
+        const float * R = part + lk_part_acc(head, 4 * half + wv, s);
+        ml[j] = *(const float2 *) (part + lk_part_ml(head, s));
+        a0[j] = *(const lk_f4 *) R;
+        a1[j] = *(const lk_f4 *) (R + 4);
     }
     float M = ml[0].x;
 #pragma unroll

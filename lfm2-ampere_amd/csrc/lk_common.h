@@ -175,6 +175,19 @@ __device__ __forceinline__ float lk_exp2(float x) {
 #endif
 }
 
+// Slice partials in `part` (fp32; lk_attn_part_bytes() holds 32 x split_cap x
+// LK_ATTN_PARTW floats, of which this layout uses 66 per (head, slot)):
+//   acc plane: [head][chunk c = dims 8c..8c+7][slot][8]  (32 x 8 x split_cap x 8)
+//   (m, l) plane after it: [head][slot][2]
+// The combine's lanes take consecutive slots, so each of its loads reads one
+// contiguous run (2 KB of acc, 512 B of (m, l)) instead of 64 records 272 B apart.
+__host__ __device__ __forceinline__ size_t lk_part_acc(int head, int c, int slot) {
+    return (((size_t) head * 8 + c) * LK_ATTN_SPLIT + slot) * 8;
+}
+__host__ __device__ __forceinline__ size_t lk_part_ml(int head, int slot) {
+    return (size_t) LK_N_HEADS * 8 * LK_ATTN_SPLIT * 8 + ((size_t) head * LK_ATTN_SPLIT + slot) * 2;
+}
+
 __host__ __device__ __forceinline__ void lk_attn_slices(int seq, int & ns, int & chunk) {
     int s = (seq + LK_ATTN_TARGET_N - 1) / LK_ATTN_TARGET_N;
     if (s < LK_ATTN_SPLIT_MIN) s = LK_ATTN_SPLIT_MIN;
