@@ -147,7 +147,7 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     if (t0 >= t1) {
         for (int i = threadIdx.x; i < LK_N_HEADS * 16; i += LK_DEC_THREADS) {
             const int h = i >> 4, k = i & 15;
-            *(lk_f4 *) (part + lk_part_acc(h, k >> 1, sp) + 4 * (k & 1)) = (lk_f4){ 0.0f, 0.0f, 0.0f, 0.0f };
+            *(lk_f4 *) (part + lk_part_acc(h, k >> 2, sp) + 4 * (k & 3)) = (lk_f4){ 0.0f, 0.0f, 0.0f, 0.0f };
         }
         if (threadIdx.x < LK_N_HEADS)
             *(float2 *) (part + lk_part_ml(threadIdx.x, sp)) = make_float2(-INFINITY, 0.0f);
@@ -411,8 +411,8 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     if (col < 4) {
         const int h = w * LK_G + col;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)          // dims 16db + 4g .. +3: chunk 2db + g/2
-            *(lk_f4 *) (part + lk_part_acc(h, 2 * db + (g >> 1), sp) + 4 * (g & 1)) = acc[db];
+        for (int db = 0; db < 4; ++db)          // dims 16db + 4g .. +3 of chunk db
+            *(lk_f4 *) (part + lk_part_acc(h, db, sp) + 4 * g) = acc[db];
         if (g == 0) *(float2 *) (part + lk_part_ml(h, sp)) = make_float2(mrun, accl[0]);
     }
 }
@@ -482,7 +482,7 @@ lk_k_attn_combine(const float * __restrict__ part, const int * __restrict__ d_po
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int s = lane + 64 * j;
-        const float * R = part + lk_part_acc(head, 4 * half + wv, s);
+        const float * R = part + lk_part_acc(head, 2 * half + (wv >> 1), s) + 8 * (wv & 1);
         ml[j] = *(const float2 *) (part + lk_part_ml(head, s));
         a0[j] = *(const lk_f4 *) R;
         a1[j] = *(const lk_f4 *) (R + 4);

@@ -177,15 +177,18 @@ __device__ __forceinline__ float lk_exp2(float x) {
 
 // Slice partials in `part` (fp32; lk_attn_part_bytes() holds 32 x split_cap x
 // LK_ATTN_PARTW floats, of which this layout uses 66 per (head, slot)):
-//   acc plane: [head][chunk c = dims 8c..8c+7][slot][8]  (32 x 8 x split_cap x 8)
+//   acc plane: [head][chunk c = dims 16c..16c+15][slot][16]  (32 x 4 x split_cap x 16)
 //   (m, l) plane after it: [head][slot][2]
-// The combine's lanes take consecutive slots, so each of its loads reads one
-// contiguous run (2 KB of acc, 512 B of (m, l)) instead of 64 records 272 B apart.
+// The combine's lanes take consecutive slots, so the four waves of a
+// (head, half) workgroup together read runs of consecutive 64-byte pieces
+// (acc; one wave 32 bytes of each) and one 512-byte run (m, l) per load,
+// instead of 64 records 272 B apart; the split's four lanes of a (head, chunk)
+// write one whole 64-byte piece.
 __host__ __device__ __forceinline__ size_t lk_part_acc(int head, int c, int slot) {
-    return (((size_t) head * 8 + c) * LK_ATTN_SPLIT + slot) * 8;
+    return (((size_t) head * 4 + c) * LK_ATTN_SPLIT + slot) * 16;
 }
 __host__ __device__ __forceinline__ size_t lk_part_ml(int head, int slot) {
-    return (size_t) LK_N_HEADS * 8 * LK_ATTN_SPLIT * 8 + ((size_t) head * LK_ATTN_SPLIT + slot) * 2;
+    return (size_t) LK_N_HEADS * LK_HEAD_DIM * LK_ATTN_SPLIT + ((size_t) head * LK_ATTN_SPLIT + slot) * 2;
 }
 
 __host__ __device__ __forceinline__ void lk_attn_slices(int seq, int & ns, int & chunk) {
