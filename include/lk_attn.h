@@ -51,7 +51,8 @@ typedef struct lk_block_q8_1 {
  * (reference kernels.cuh:630-635, retuned for 256 CUs). */
 int lk_attn_config(int * split_cap, int * target_n, int * split_min);
 
-/* Bytes the caller must allocate for `part` (fp32 [32][split_cap][68]).
+/* Bytes the caller must allocate for `part` (32 x split_cap x 68 fp32; the
+ * layout inside is the library's own).
  * Replaces the engine's own sizing at reference engine.cu:408-409. */
 size_t lk_attn_part_bytes(void);
 
