@@ -342,7 +342,10 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         // nki + xs = nkj - xs balances the groups; B's first tile must not lie
         // past bj's first query, so that every row of bj sees a key in B's part
         // (A's part starts at key 0)
-        xs = (nkj - nki) / 2;
+        // (with an odd tile count the fp16 kernel gives the odd tile to A, which
+        // measured faster -- B merges A's part at the end; the int8 kernel
+        // measured faster with it in B)
+        xs = (nkj - nki + (INT8 ? 0 : 1)) / 2;
         const int kdj = (P + bj * PF_BQ) / PF_BK;
         if (xs > kdj) xs = kdj;
         if (xs < 0) xs = 0;
