@@ -463,6 +463,9 @@ __device__ __forceinline__ void lk_quant_q8_1_half(float x, lk_block_q8_1 * __re
 // run-to-run bit-identical.  Each half is exactly one Q8_1 block of the next
 // GEMV's input.
 static_assert(LK_ATTN_SPLIT <= 256 && LK_ATTN_SPLIT % 64 == 0, "combine: 1-4 whole slots per lane");
+static_assert(lk_part_ml(LK_N_HEADS - 1, LK_ATTN_SPLIT - 1) + 2 <= (size_t) LK_N_HEADS * LK_ATTN_SPLIT * LK_ATTN_PARTW &&
+              lk_part_acc(LK_N_HEADS - 1, 3, LK_ATTN_SPLIT - 1) + 16 <= lk_part_ml(0, 0),
+              "the partial layout fits lk_attn_part_bytes() and its planes do not overlap");
 __global__ void __launch_bounds__(256)
 lk_k_attn_combine(const float * __restrict__ part, const int * __restrict__ d_pos,
                   float * __restrict__ out, lk_block_q8_1 * __restrict__ yq8, int * __restrict__ advance) {

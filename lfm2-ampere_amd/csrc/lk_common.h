@@ -184,10 +184,10 @@ __device__ __forceinline__ float lk_exp2(float x) {
 // (acc; one wave 32 bytes of each) and one 512-byte run (m, l) per load,
 // instead of 64 records 272 B apart; the split's four lanes of a (head, chunk)
 // write one whole 64-byte piece.
-__host__ __device__ __forceinline__ size_t lk_part_acc(int head, int c, int slot) {
+__host__ __device__ constexpr size_t lk_part_acc(int head, int c, int slot) {
     return (((size_t) head * 4 + c) * LK_ATTN_SPLIT + slot) * 16;
 }
-__host__ __device__ __forceinline__ size_t lk_part_ml(int head, int slot) {
+__host__ __device__ constexpr size_t lk_part_ml(int head, int slot) {
     return (size_t) LK_N_HEADS * LK_HEAD_DIM * LK_ATTN_SPLIT + ((size_t) head * LK_ATTN_SPLIT + slot) * 2;
 }
 
