@@ -34,7 +34,10 @@ extern "C" {
 #define LK_N_HEADS      32
 #define LK_N_KV_HEADS   8
 #define LK_HEAD_DIM     64
-#define LK_ATTN_PARTW   (4 + LK_HEAD_DIM)   /* partial record: m, l, 2 pad, acc[64] */
+/* fp32 words per (query head, slot) of the decode partial buffer: it only sizes
+ * that buffer (lk_attn_part_bytes); the layout inside is private to the
+ * library (an acc plane and an (m, l) plane, not one record per slot). */
+#define LK_ATTN_PARTW   (4 + LK_HEAD_DIM)
 
 /* Q8_1 activation block (reference quant.cuh:27-31): fp16 d = amax/127 and
  * fp16 raw sum of the 32 values, then the 32 int8 quants.  36 bytes. */
@@ -235,14 +238,35 @@ int lk_pf_attn_q81(const void * qh, int m, int P, const void * kc, const void * 
 int lk_pf_quant_rows(const float * X, int rows, int ld, int kb, int8_t * qs, float * sc,
                      void * stream);
 
+/* The same attention entry points with a caller-owned workspace for the
+ * split-K partials, the reference's convention that every buffer is the
+ * engine's (engine.cu:974-985): work (16-byte aligned device memory) of
+ * work_bytes bytes; lk_pf_part_bytes() (64 MiB) is the most any chunk uses, a
+ * smaller workspace makes the planner cut coarser pieces (work_bytes 0: no
+ * split).  Launches that share one workspace must be ordered (one stream, or
+ * the caller's events), as in the reference; with its own workspace every
+ * launch may be captured into a hipGraph.  work = NULL falls back to the
+ * library's static scratch (below).  No counterpart in the reference (its
+ * kernels do not split). */
+size_t lk_pf_part_bytes(void);
+int lk_pf_attn8_ws(const int8_t * q8, const float * qsc, const float * qcs,
+                   const void * qh, int m, int P, const int8_t * k8,
+                   const float * ksc, int kstride, const void * kc,
+                   const void * vc, int near, int sink, float * o,
+                   int8_t * aqs, float * asc, void * work, size_t work_bytes, void * stream);
+int lk_pf_attn_ws(const void * qh, int m, int P, const void * kc, const void * vc,
+                  float * o, int8_t * aqs, float * asc, void * work, size_t work_bytes,
+                  void * stream);
+
 /* Both attention entry points balance causal chunks by splitting the key range
  * of long query blocks across workgroups (merged by a second kernel, in a fixed
- * order: output stays run-to-run bit-identical).  The split uses a static
- * 64 MiB device scratch of the library; calls on one device that overlap in
- * time (different streams) must not both split.  Process-wide knob, for tests
- * and tuning: -1 never split, 0 automatic (default), n > 0 parts of at most n
- * key tiles of 64.  No counterpart in the reference (its kernels do not
- * split). */
+ * order: output stays run-to-run bit-identical).  The entry points without a
+ * workspace put the partials in a static 64 MiB device scratch of the library;
+ * a split launch from another stream while an earlier one on that device is
+ * pending is refused with hipErrorNotReady (not checked under stream capture).
+ * Process-wide knob, for tests and tuning: -1 never split, 0 automatic
+ * (default), n > 0 parts of at most n key tiles of 64.  No counterpart in the
+ * reference (its kernels do not split). */
 int lk_pf_split_override(int tiles);
 
 /* Paired launches: one 8-wave workgroup per (kv head, block pair i, nq-1-i) of
@@ -254,6 +278,17 @@ int lk_pf_split_override(int tiles);
  * whenever the chunk has two or more blocks.  No counterpart in the
  * reference. */
 int lk_pf_pair_override(int mode);
+
+/* The paired kernel's two 4-wave groups meet at barriers of their own (a
+ * counter in LDS), each polled at most `polls` times so that no wave can hang
+ * the kernel (default 2^22 polls, about a quarter second per barrier; 0 sets
+ * the default back).  A barrier that gives up is counted per device and makes
+ * every output its workgroup writes afterwards NaN; the kernel still runs to
+ * its end.  lk_pf_gsync_faults reads that count (synchronously: a diagnostic,
+ * not for graph capture) and clears it when reset != 0.  Process-wide test
+ * hooks; no counterpart in the reference. */
+int lk_pf_gsync_limit(int polls);
+int lk_pf_gsync_faults(unsigned * count, int reset);
 
 /* ---- attention-input producers ---------------------------------------------
  * Per-head RMS norm (eps 1e-5) of q and k with weights qn / kn (fp32 [64]),

@@ -605,10 +605,15 @@ static int lk_combine_launch(const float * part, const int * d_pos, float * out,
     return lk_launch_status("lk_attn_combine");
 }
 
+// The split kernel reads q with 16-byte loads (lk_ld16_untracked).
+static bool lk_q_misaligned(const float * q) { return ((uintptr_t) q & 15u) != 0; }
+
 extern "C" int lk_attn_split(const float * q, const void * kc, const void * vc,
                              const int * d_pos, float * part, void * stream) {
     if (!q || !kc || !vc || !d_pos || !part)
         return lk_fail(hipErrorInvalidValue, "lk_attn_split: null pointer argument");
+    if (lk_q_misaligned(q))
+        return lk_fail(hipErrorInvalidValue, "lk_attn_split: q must be 16-byte aligned");
     return lk_split_launch(q, kc, vc, d_pos, part, lk_stream(stream));
 }
 
@@ -639,29 +644,79 @@ extern "C" int lk_attn_decode(const float * q, const void * kc, const void * vc,
 #define LK_DEC_SCRATCH_FLOATS ((size_t) LK_N_HEADS * LK_ATTN_SPLIT * LK_ATTN_PARTW)
 static __device__ __align__(256) float scratch[LK_DEC_SCRATCH_FLOATS];
 
-static float * lk_dec_scratch_ptr(int & err) {
-    static std::mutex mu;
-    static float * ptr[LK_MAX_DEVICES] = {};
+// Per device: the array's device address, and the guard of its single-stream
+// use -- the stream of the last call and an event recorded after its combine.
+// A call from another stream while that event is pending would overwrite
+// partials the earlier call has not merged yet; it is refused
+// (hipErrorNotReady) instead.  Calls on one stream are ordered and always
+// accepted.  Under stream capture nothing is checked or recorded (the graph's
+// own order decides).  Address and event are set up on a device's first call.
+struct LkDecScratchUse {
+    float * ptr = nullptr;
+    hipStream_t last = nullptr;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+};
+static std::mutex g_dec_mu;
+static LkDecScratchUse g_dec_use[LK_MAX_DEVICES];
+
+static bool lk_capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    (void) hipStreamIsCapturing(st, &cs);
+    return cs != hipStreamCaptureStatusNone;
+}
+
+static float * lk_dec_scratch_acquire(hipStream_t st, int & err, int & dev_out) {
     int dev = 0;
-    const hipError_t e = hipGetDevice(&dev);
+    hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess || dev < 0 || dev >= LK_MAX_DEVICES) {
         err = lk_fail(e != hipSuccess ? (int) e : (int) hipErrorInvalidDevice,
                       "lk_attn_decode_noalloc: no usable current device");
         return nullptr;
     }
-    std::lock_guard<std::mutex> lock(mu);
-    if (!ptr[dev]) {
+    std::lock_guard<std::mutex> lock(g_dec_mu);
+    LkDecScratchUse & u = g_dec_use[dev];
+    if (!u.ptr) {
         void * p = nullptr;
-        const hipError_t g = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (g != hipSuccess || !p) {
-            err = lk_fail(g != hipSuccess ? (int) g : (int) hipErrorInvalidSymbol,
-                          "lk_attn_decode_noalloc: scratch lookup on device %d: %s", dev, hipGetErrorString(g));
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            err = lk_fail(e != hipSuccess ? (int) e : (int) hipErrorInvalidSymbol,
+                          "lk_attn_decode_noalloc: scratch lookup on device %d: %s", dev, hipGetErrorString(e));
             return nullptr;
         }
-        ptr[dev] = (float *) p;
+        e = hipEventCreateWithFlags(&u.done, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            err = lk_fail((int) e, "lk_attn_decode_noalloc: guard event: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        u.ptr = (float *) p;
+    }
+    if (!lk_capturing(st) && u.pending && u.last != st) {
+        e = hipEventQuery(u.done);
+        (void) hipGetLastError();                     // the query's status is not a launch error
+        if (e == hipErrorNotReady) {
+            err = lk_fail(hipErrorNotReady,
+                          "lk_attn_decode_noalloc: a call on another stream of device %d is still pending; "
+                          "calls share one partial array per device: order them on one stream "
+                          "(or wait for the earlier one)", dev);
+            return nullptr;
+        }
     }
     err = 0;
-    return ptr[dev];
+    dev_out = dev;
+    return u.ptr;
+}
+
+// After the combine is enqueued on st: mark the array busy until it completes.
+static int lk_dec_scratch_release(hipStream_t st, int dev) {
+    if (lk_capturing(st)) return 0;
+    std::lock_guard<std::mutex> lock(g_dec_mu);
+    LkDecScratchUse & u = g_dec_use[dev];
+    const hipError_t e = hipEventRecord(u.done, st);
+    if (e != hipSuccess) return lk_fail((int) e, "lk_attn_decode_noalloc: guard record: %s", hipGetErrorString(e));
+    u.last = st;
+    u.pending = true;
+    return 0;
 }
 
 extern "C" int lk_attn_decode_noalloc(const float * q, const void * kc, const void * vc,
@@ -671,13 +726,17 @@ extern "C" int lk_attn_decode_noalloc(const float * q, const void * kc, const vo
                   "scratch holds one full partial set");
     if (!q || !kc || !vc || !d_pos)
         return lk_fail(hipErrorInvalidValue, "lk_attn_decode_noalloc: null pointer argument");
-    int err = 0;
-    float * part = lk_dec_scratch_ptr(err);
-    if (!part) return err;
+    if (lk_q_misaligned(q))
+        return lk_fail(hipErrorInvalidValue, "lk_attn_decode_noalloc: q must be 16-byte aligned");
     hipStream_t st = lk_stream(stream);
+    int err = 0, dev = 0;
+    float * part = lk_dec_scratch_acquire(st, err, dev);
+    if (!part) return err;
     int rc = lk_split_launch(q, kc, vc, d_pos, part, st);
     if (rc) return rc;
-    return lk_combine_launch(part, d_pos, out, yq8, st);
+    rc = lk_combine_launch(part, d_pos, out, yq8, st);
+    if (rc) return rc;
+    return lk_dec_scratch_release(st, dev);
 }
 
 extern "C" int lk_attention_decode(const float * q, const void * kc, const void * vc,
@@ -711,9 +770,12 @@ extern "C" int lk_decode_graph_create(int n_layers, const float * const * q,
         return lk_fail(hipErrorInvalidValue, "lk_decode_graph_create: bad arguments");
     if (!stream)
         return lk_fail(hipErrorInvalidValue, "lk_decode_graph_create: capture needs a non-default stream");
-    for (int i = 0; i < n_layers; ++i)
+    for (int i = 0; i < n_layers; ++i) {
         if (!q[i] || !kc[i] || !vc[i])
             return lk_fail(hipErrorInvalidValue, "lk_decode_graph_create: null pointer for layer %d", i);
+        if (lk_q_misaligned(q[i]))
+            return lk_fail(hipErrorInvalidValue, "lk_decode_graph_create: q of layer %d must be 16-byte aligned", i);
+    }
     hipStream_t st = lk_stream(stream);
     hipError_t e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
     if (e != hipSuccess) return lk_fail((int) e, "hipStreamBeginCapture: %s", hipGetErrorString(e));
@@ -751,6 +813,10 @@ extern "C" int lk_decode_step_graph_create(int n_layers, const lk_decode_layer *
         const lk_decode_layer & L = layers[i];
         if (!L.q_src || !L.k_src || !L.v_src || !L.q || !L.k || !L.q_norm || !L.k_norm || !L.kc || !L.vc)
             return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: null pointer for layer %d", i);
+        if (lk_q_misaligned(L.q_src) || lk_q_misaligned(L.k_src) || lk_q_misaligned(L.v_src)
+            || lk_q_misaligned(L.q_norm) || lk_q_misaligned(L.k_norm))
+            return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: layer %d: q_src, k_src, v_src, "
+                           "q_norm and k_norm must be 16-byte aligned (16-byte loads)", i);
         if (L.wo_qs && (!L.wo_d || !L.x || !L.yq8))
             return lk_fail(hipErrorInvalidValue, "lk_decode_step_graph_create: layer %d: the output projection needs wo_d, x and yq8", i);
     }

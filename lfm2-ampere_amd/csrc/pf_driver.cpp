@@ -12,7 +12,10 @@
 //      that follows, engine.cu:1126, fused into the attention epilogue);
 //      without smoothing the attention kernel quantises Q itself (same bits).
 // lk_pf_chunk_done(pos0 + m) after the chunk's last layer moves k8_valid,
-// exactly where the reference does.  Buffers are allocated once, at create.
+// exactly where the reference does.  Buffers are allocated once, at create,
+// the split-K partial workspace of the attention launches included, so that a
+// context owns every buffer its launches touch (engine.cu:974-985) and the
+// launches of two contexts never share scratch.
 #include "lk_common.h"
 #include <vector>
 
@@ -23,6 +26,8 @@ struct lk_pf_ctx {
     _Float16 * qh = nullptr;
     int8_t * q8 = nullptr;
     float * qsc = nullptr, * qcs = nullptr;
+    void * work = nullptr;                               // split-K partials (lk_pf_part_bytes())
+    size_t work_bytes = 0;
     std::vector<int8_t *> k8;
     std::vector<float *> ksc, cm;
 };
@@ -30,6 +35,7 @@ struct lk_pf_ctx {
 static void pf_ctx_free(lk_pf_ctx * c) {
     if (!c) return;
     (void) hipFree(c->qh); (void) hipFree(c->q8); (void) hipFree(c->qsc); (void) hipFree(c->qcs);
+    (void) hipFree(c->work);
     for (auto p : c->k8) (void) hipFree(p);
     for (auto p : c->ksc) (void) hipFree(p);
     for (auto p : c->cm) (void) hipFree(p);
@@ -53,6 +59,8 @@ extern "C" int lk_pf_ctx_create(int n_layers, int max_chunk, int max_seq, int at
     c->kstride = (max_seq + 3) & ~3;                     // engine.cu:249 (ksc row stride)
     c->attn8 = attn8 != 0; c->ksmooth = ksmooth != 0; c->near = near; c->sink = sink;
     bool ok = pf_alloc(&c->qh, (size_t) max_chunk * LK_HIDDEN);
+    c->work_bytes = lk_pf_part_bytes();
+    ok = ok && pf_alloc((char **) &c->work, c->work_bytes);
     if (c->attn8) {
         ok = ok && pf_alloc(&c->q8, (size_t) max_chunk * LK_HIDDEN) && pf_alloc(&c->qsc, (size_t) max_chunk * LK_N_HEADS)
                 && pf_alloc(&c->qcs, (size_t) max_chunk * LK_N_HEADS);
@@ -79,7 +87,7 @@ extern "C" int lk_pf_chunk_attn(lk_pf_ctx * c, int layer, const float * Y, const
     int rc;
     if (!c->attn8) {
         rc = lk_pf_qknr(Y, qn, kn, m, pos0, c->qh, kc, vc, nullptr, nullptr, 0, nullptr, stream);
-        return rc ? rc : lk_pf_attn_q81(c->qh, m, pos0, kc, vc, o, aqs, asc, stream);
+        return rc ? rc : lk_pf_attn_ws(c->qh, m, pos0, kc, vc, o, aqs, asc, c->work, c->work_bytes, stream);
     }
     int8_t * k8 = c->k8[layer];
     float * ksc = c->ksc[layer];
@@ -99,12 +107,12 @@ extern "C" int lk_pf_chunk_attn(lk_pf_ctx * c, int layer, const float * Y, const
     }
     if (rc) return rc;
     if (!cm)   // no smoothing: the attention kernel quantises Q itself (same bits, one pass less)
-        return lk_pf_attn8_q81(nullptr, nullptr, nullptr, c->qh, m, pos0, k8, ksc, c->kstride, kc, vc,
-                               c->near, c->sink, o, aqs, asc, stream);
+        return lk_pf_attn8_ws(nullptr, nullptr, nullptr, c->qh, m, pos0, k8, ksc, c->kstride, kc, vc,
+                              c->near, c->sink, o, aqs, asc, c->work, c->work_bytes, stream);
     rc = lk_pf_q8(c->qh, m, cm, c->q8, c->qsc, c->qcs, stream);
     if (rc) return rc;
-    return lk_pf_attn8_q81(c->q8, c->qsc, c->qcs, c->qh, m, pos0, k8, ksc, c->kstride, kc, vc,
-                           c->near, c->sink, o, aqs, asc, stream);
+    return lk_pf_attn8_ws(c->q8, c->qsc, c->qcs, c->qh, m, pos0, k8, ksc, c->kstride, kc, vc,
+                          c->near, c->sink, o, aqs, asc, c->work, c->work_bytes, stream);
 }
 
 extern "C" int lk_pf_chunk_done(lk_pf_ctx * c, int pos_end) {

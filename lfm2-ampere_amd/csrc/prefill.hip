@@ -30,6 +30,7 @@
 #include <math.h>
 #include <algorithm>
 #include <type_traits>
+#include <atomic>
 #include <mutex>
 
 // ---------------------------------------------------------------------------
@@ -150,15 +151,9 @@ __host__ __device__ __forceinline__ bool lk_pf_exact(int P, int qt32, int kt64, 
     return (kt64 * 64 + 64 > P + qt32 * 32 - near) || (sink && kt64 == 0);
 }
 
-// The int32 S^T block of 16 keys x 16 queries over the full head_dim: A = 16
-// key rows (lane l: key l%16, bytes 16g..16g+15), B = Q^T (lane l: query l%16,
-// the same bytes).  Shared by the attention kernel and the test hook.
-__device__ __forceinline__ lk_i4 lk_mfma_qk8(lk_i4 kfrag, lk_i4 qfrag) {
-    const lk_i4 z = { 0, 0, 0, 0 };
-    return __builtin_amdgcn_mfma_i32_16x16x64_i8(kfrag, qfrag, z, 0, 0, 0);
-}
-
-// The same block with the accumulator seeded by the bit pattern of
+// The int32 S^T block of 16 keys x 16 queries over the full head_dim (A = 16
+// key rows, lane l: key l%16, bytes 16g..16g+15; B = Q^T, lane l: query l%16,
+// the same bytes), with the accumulator seeded by the bit pattern of
 // PF_MAGIC = 1.5 * 2^23: |sum| <= 64 * 128 * 128 < 2^22, so the integer result
 // is the fp32 bit pattern of PF_MAGIC + sum, exactly (the float conversion done
 // by the integer add inside the MFMA).  sum * ks is then one fma,
@@ -205,6 +200,7 @@ static inline void pf_parts(int qt, int m, int P, int lsplit, int & np, int & pe
 #define PF_MAX_QB    128
 struct PfWork {
     int n_items, n_split;                              // n_items 0: unsplit launch
+    int spin;                                          // PAIR: poll bound of a group barrier
     uint32_t item[PF_MAX_ITEMS];                       // qt | (partial slot + 1) << 16 (0: not split)
     uint32_t krange[PF_MAX_ITEMS];                     // kt_lo | kt_hi << 16
     int16_t slot0[PF_MAX_QB];
@@ -216,9 +212,13 @@ struct PfWork {
 // then (m, l) as [head][64 rows] of float2; m is in the log2 domain of p.
 #define PF_PART_ACC   (LK_G * 16 * PF_BQ * 4)           // floats
 #define PF_PART_SLOT  (PF_PART_ACC + LK_G * PF_BQ * 2)  // floats per (part, kv head)
-// Static scratch for the partials, 64 MiB per device.
+// Static scratch for the partials, 64 MiB per device: the fallback of launches
+// that bring no workspace of their own.
 #define PF_PART_CAP   (16u << 20)                        // floats
 __device__ float g_pf_part[PF_PART_CAP];
+// Group barriers of the paired kernel that gave up waiting (poll bound spent),
+// counted per device; the workgroup's outputs are then NaN.
+__device__ unsigned g_pf_gsync_fault;
 
 // ---- planar Q8_1 of the attention output (the next GEMM's input) -------------
 // Reference k_pf_quant_rows / pf_quant_warp (prefill.cu:1574-1580, 90-103): per
@@ -326,6 +326,9 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // then pair a long block with a short one.  Split launches: one work item
     // (block, key range) per workgroup, longest first.
     const int tid  = threadIdx.x;
+#ifdef PF_AGPR
+    asm volatile("; agpr" :: "a"(0));
+#endif
     const int lane = tid & 63;
     const int w    = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col  = lane & 15, g = lane >> 4;
@@ -473,24 +476,36 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         issue_to(kt, 2 * grp + (it & 1), mode_at(kt, g_base(it)));
     };
     // PAIR: the group barrier, a counter per group in LDS that only grows
-    // (4 arrivals per step); the poll is bounded so that a wave can never
-    // hang the kernel.
+    // (4 arrivals per step); the poll is bounded (work.spin polls) so that a
+    // wave can never hang the kernel.  A wave that gives up marks its group
+    // (s_gbad) and counts the event in g_pf_gsync_fault: the group may then
+    // have read a tile stage before all of its rows were in, so every output
+    // the group writes afterwards is NaN, and the host can read the count
+    // (lk_pf_gsync_faults).  The kernel still runs to its end.
     __shared__ unsigned s_gbar[2];
+    __shared__ unsigned s_gbad[2];
     unsigned g_gen = 0;
     auto gsync = [&]() {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (lane == 0) __hip_atomic_fetch_add(&s_gbar[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         g_gen += 4;
-        for (int n = 0; n < (1 << 22); ++n) {
+        bool met = false;
+        for (int n = 0; n < work.spin; ++n) {
             const unsigned c = __builtin_amdgcn_readfirstlane(
                 __hip_atomic_load(&s_gbar[grp], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
-            if ((int) (c - g_gen) >= 0) break;
+            if ((int) (c - g_gen) >= 0) { met = true; break; }
             __builtin_amdgcn_s_sleep(1);
+        }
+        if (!met) {                                   // wave-uniform
+            if (lane == 0) {
+                __hip_atomic_store(&s_gbad[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                __hip_atomic_fetch_add(&g_pf_gsync_fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     };
     if constexpr (PAIR) {
-        if (tid < 2) s_gbar[tid] = 0u;
+        if (tid < 2) { s_gbar[tid] = 0u; s_gbad[tid] = 0u; }
         // (the workgroup barrier after the Q prologue below orders this
         // before every group barrier)
     }
@@ -870,9 +885,14 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 
     // ---- epilogue: l over the 4 lane groups, then o[q][head*64 + d] -------------
     auto emit = [&]() {
+        // PAIR: NaN outputs when a group barrier of this workgroup gave up
+        bool poison = false;
+        if constexpr (PAIR)
+            poison = (__hip_atomic_load(&s_gbad[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) |
+                      __hip_atomic_load(&s_gbad[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) != 0u;
 #pragma unroll
         for (int qb = 0; qb < PF_QB; ++qb) {
-            const float il = 1.0f / acc[4][qb][0];
+            const float il = poison ? __builtin_nanf("") : 1.0f / acc[4][qb][0];
             const int qr = qbase + 16 * qb + col;
             lk_f4 a[4];
 #pragma unroll
@@ -1085,7 +1105,11 @@ lk_k_pf_quant_rows(const float * __restrict__ X, int ld, int kb, int8_t * __rest
     if (lane == 0) sc[(size_t) r * kb + b] = lk_q81_scales(d, sum);
 }
 
-// Test hook: s[h][i][j] = int32 q8[i][h] . k8[j][h/4], one wave per 16x16 block.
+// Test hook: s[h][i][j] = int32 q8[i][h] . k8[j][h/4], one wave per 16x16 block,
+// by the routine the attention kernel scores int8 tiles with: the MFMA seeded
+// with the bit pattern of PF_MAGIC, its result read back as fp32 PF_MAGIC + sum,
+// returned as (bits - 0x4B400000), which equals the integer sum exactly while
+// |sum| < 2^22 (the int8 bound is 64 * 128 * 128 = 2^20).
 __global__ void __launch_bounds__(64)
 lk_k_pf_qk_i32(const int8_t * __restrict__ q8, int m, const int8_t * __restrict__ k8, int n,
                int32_t * __restrict__ s) {
@@ -1093,10 +1117,13 @@ lk_k_pf_qk_i32(const int8_t * __restrict__ q8, int m, const int8_t * __restrict_
     const int lane = threadIdx.x, col = lane & 15, g = lane >> 4;
     const lk_i4 kf = *(const lk_i4 *) (k8 + ((size_t) (j0 + col) * LK_N_KV_HEADS + h / LK_G) * LK_HEAD_DIM + 16 * g);
     const lk_i4 qf = *(const lk_i4 *) (q8 + (size_t) (i0 + col) * LK_HIDDEN + h * LK_HEAD_DIM + 16 * g);
-    const lk_i4 c = lk_mfma_qk8(kf, qf);         // c[r] = S^T[key j0+4g+r][query i0+col]
+    // c[r] = PF_MAGIC + S^T[key j0+4g+r][query i0+col].  The whole vector is
+    // reinterpreted, not an element: this compiler lowers __builtin_bit_cast of
+    // a vector element (c[r]) to a load of element 0 for every r.
+    const lk_i4 c = __builtin_bit_cast(lk_i4, lk_mfma_qk8_magic(kf, qf));
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-        s[((size_t) h * m + i0 + col) * n + j0 + 4 * g + r] = c[r];
+        s[((size_t) h * m + i0 + col) * n + j0 + 4 * g + r] = c[r] - 0x4B400000;
 }
 
 // ---------------------------------------------------------------------------
@@ -1134,14 +1161,41 @@ extern "C" int lk_pf_kmean(const void * kc, int n, float * cm, void * stream) {
 }
 
 // ---- host: split choice -------------------------------------------------------
+// Process-wide tuning knobs, atomics so that calls from several host threads
+// may read them while a test sets them; each launch reads each knob once.
 // -1: never split, 0: automatic, > 0: parts of at most that many tiles (test hook)
-static int g_pf_split_override = 0;
+static std::atomic<int> g_pf_split_override{0};
+// Poll bound of the paired kernel's group barrier (test hook; the default
+// leaves ample time: a group waits for its slowest wave of one tile step,
+// microseconds, while 2^22 polls of s_sleep 1 take about a quarter second).
+#define PF_GSYNC_SPIN_DEFAULT (1 << 22)
+static std::atomic<int> g_pf_gsync_spin{PF_GSYNC_SPIN_DEFAULT};
 
 extern "C" int lk_pf_split_override(int tiles) {
     if (tiles < -1) return lk_fail(hipErrorInvalidValue, "lk_pf_split_override: %d < -1", tiles);
-    g_pf_split_override = tiles;
+    g_pf_split_override.store(tiles, std::memory_order_relaxed);
     return 0;
 }
+
+extern "C" int lk_pf_gsync_limit(int polls) {
+    if (polls < 0) return lk_fail(hipErrorInvalidValue, "lk_pf_gsync_limit: %d < 0", polls);
+    g_pf_gsync_spin.store(polls == 0 ? PF_GSYNC_SPIN_DEFAULT : polls, std::memory_order_relaxed);
+    return 0;
+}
+
+extern "C" int lk_pf_gsync_faults(unsigned * count, int reset) {
+    if (!count) return lk_fail(hipErrorInvalidValue, "lk_pf_gsync_faults: count is null");
+    hipError_t e = hipMemcpyFromSymbol(count, HIP_SYMBOL(g_pf_gsync_fault), sizeof(unsigned), 0, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return lk_fail((int) e, "lk_pf_gsync_faults: %s", hipGetErrorString(e));
+    if (reset) {
+        const unsigned z = 0;
+        e = hipMemcpyToSymbol(HIP_SYMBOL(g_pf_gsync_fault), &z, sizeof z, 0, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return lk_fail((int) e, "lk_pf_gsync_faults: %s", hipGetErrorString(e));
+    }
+    return 0;
+}
+
+extern "C" size_t lk_pf_part_bytes(void) { return (size_t) PF_PART_CAP * sizeof(float); }
 
 // Device address of the partial scratch, per device (looked up once), and the
 // guard of its single-stream use: the stream of the last splitting launch on
@@ -1236,10 +1290,11 @@ static int pf_slots_per_device() {
 #ifndef PF_PLAN_T
 #define PF_PLAN_T 1.0f      // piece cost, in units of the mean cost per slot
 #endif
-static void pf_plan(int m, int P, int near, int sink, bool int8, PfWork & wk) {
+static void pf_plan(int m, int P, int near, int sink, bool int8, int split_override, size_t cap_floats,
+                    PfWork & wk) {
     wk.n_items = 0; wk.n_split = 0;
     const int nq = (m + PF_BQ - 1) / PF_BQ;
-    if (g_pf_split_override < 0 || nq > PF_MAX_QB) return;
+    if (split_override < 0 || nq > PF_MAX_QB) return;
     auto tcost = [&](int qt, int kt) -> float {
         return (!int8 || lk_pf_exact(P, 2 * qt, kt, near, sink)) ? 1.4f : 1.0f;
     };
@@ -1262,10 +1317,10 @@ static void pf_plan(int m, int P, int near, int sink, bool int8, PfWork & wk) {
     auto fits = [&]() {
         int items = 0, parts = 0;
         for (int qt = 0; qt < nq; ++qt) { items += npc[qt]; if (npc[qt] > 1) parts += npc[qt]; }
-        return items <= PF_MAX_ITEMS && (size_t) parts * LK_N_KV_HEADS * PF_PART_SLOT <= PF_PART_CAP;
+        return items <= PF_MAX_ITEMS && (size_t) parts * LK_N_KV_HEADS * PF_PART_SLOT <= cap_floats;
     };
-    if (g_pf_split_override > 0) {                     // equal parts of at most L tiles
-        for (int L = g_pf_split_override;; L *= 2) {
+    if (split_override > 0) {                          // equal parts of at most L tiles
+        for (int L = split_override;; L *= 2) {
             bool ok = true;
             for (int qt = 0; qt < nq; ++qt) {
                 int np, per;
@@ -1335,7 +1390,7 @@ static void pf_plan(int m, int P, int near, int sink, bool int8, PfWork & wk) {
 extern "C" int lk_pf_plan_items(int m, int P, int near, int sink, int int8, int32_t * items, int max_items) {
     if (m < 1 || P < 0 || max_items < 0 || (!items && max_items > 0)) return -1;
     PfWork wk;
-    pf_plan(m, P, near, sink, int8 != 0, wk);
+    pf_plan(m, P, near, sink, int8 != 0, g_pf_split_override.load(std::memory_order_relaxed), PF_PART_CAP, wk);
     for (int i = 0; i < wk.n_items && i < max_items; ++i) {
         items[4 * i + 0] = (int32_t) (wk.item[i] & 255);
         items[4 * i + 1] = (int32_t) (wk.krange[i] & 0xffff);
@@ -1347,11 +1402,11 @@ extern "C" int lk_pf_plan_items(int m, int P, int near, int sink, int int8, int3
 
 // Paired launches (8-wave workgroups over blocks i and nq-1-i): -1 never,
 // 0 automatic, 1 whenever the chunk has at least two query blocks (test hook).
-static int g_pf_pair_override = 0;
+static std::atomic<int> g_pf_pair_override{0};
 
 extern "C" int lk_pf_pair_override(int mode) {
     if (mode < -1 || mode > 1) return lk_fail(hipErrorInvalidValue, "lk_pf_pair_override: %d not in -1..1", mode);
-    g_pf_pair_override = mode;
+    g_pf_pair_override.store(mode, std::memory_order_relaxed);
     return 0;
 }
 
@@ -1362,20 +1417,23 @@ extern "C" int lk_pf_pair_override(int mode) {
 // P = 4096 int8 265.7 against 271.5, fp16 254.1 against 279.5.  Deep chunks
 // keep the split plan (P = 126976: int8 4383 us paired against 3862, fp16
 // 4397 against 4173).  Not under a forced split size.
-static bool pf_use_pair(int m, int P) {
+static bool pf_use_pair(int m, int P, int pair_override, int split_override) {
     const int nq = (m + PF_BQ - 1) / PF_BQ;
-    if (g_pf_pair_override < 0 || nq < 2) return false;
-    if (g_pf_pair_override > 0) return true;
-    return g_pf_split_override <= 0 && P <= m && nq >= 64;
+    if (pair_override < 0 || nq < 2) return false;
+    if (pair_override > 0) return true;
+    return split_override <= 0 && P <= m && nq >= 64;
 }
 
 template <bool INT8, bool Q81>
 static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qcs, const _Float16 * qh,
                           int m, int P, const int8_t * k8, const float * ksc, int kstride,
                           const _Float16 * kc, const _Float16 * vc, int near, int sink, float * o,
-                          int8_t * aqs, float2 * asc, hipStream_t st, const char * what) {
+                          int8_t * aqs, float2 * asc, float * work, size_t work_bytes, hipStream_t st,
+                          const char * what) {
     PfWork wk;
-    if (pf_use_pair(m, P)) {
+    wk.spin = g_pf_gsync_spin.load(std::memory_order_relaxed);
+    const int split_override = g_pf_split_override.load(std::memory_order_relaxed);
+    if (pf_use_pair(m, P, g_pf_pair_override.load(std::memory_order_relaxed), split_override)) {
         wk.n_items = 0; wk.n_split = 0;
         const int npairs = ((m + PF_BQ - 1) / PF_BQ + 1) / 2;
         hipLaunchKernelGGL((lk_k_pf_attn<INT8, true, Q81>), dim3(npairs * LK_N_KV_HEADS), dim3(512), 0, st,
@@ -1383,7 +1441,10 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
                            (float *) nullptr);
         return lk_launch_status(what);
     }
-    pf_plan(m, P, near, sink, INT8, wk);
+    // a caller workspace bounds the partials the plan may write (a smaller one
+    // gives coarser pieces, none at all an unsplit launch); without one the
+    // library's static scratch is used
+    pf_plan(m, P, near, sink, INT8, split_override, work ? work_bytes / sizeof(float) : (size_t) PF_PART_CAP, wk);
     if (wk.n_items == 0) {
         hipLaunchKernelGGL((lk_k_pf_attn<INT8, false, Q81>), dim3((m + PF_BQ - 1) / PF_BQ, LK_N_KV_HEADS), dim3(256), 0, st,
                            q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk,
@@ -1391,7 +1452,7 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
         return lk_launch_status(what);
     }
     int err = 0, dev = 0;
-    float * pbuf = pf_part_acquire(st, err, dev);
+    float * pbuf = work ? work : pf_part_acquire(st, err, dev);
     if (!pbuf) return err;
     hipLaunchKernelGGL((lk_k_pf_attn<INT8, false, Q81>), dim3(wk.n_items * LK_N_KV_HEADS), dim3(256), 0, st,
                        q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, wk, pbuf);
@@ -1401,15 +1462,17 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
                        (const float *) pbuf, m, P, wk, o, aqs, asc);
     rc = lk_launch_status(what);
     if (rc) return rc;
-    return pf_part_release(st, dev);
+    return work ? 0 : pf_part_release(st, dev);      // a caller's workspace is ordered by the caller
 }
 
-extern "C" int lk_pf_attn8_q81(const int8_t * q8, const float * qsc, const float * qcs,
-                               const void * qh, int m, int P, const int8_t * k8,
-                               const float * ksc, int kstride, const void * kc,
-                               const void * vc, int near, int sink, float * o,
-                               int8_t * aqs, float * asc, void * stream) {
+extern "C" int lk_pf_attn8_ws(const int8_t * q8, const float * qsc, const float * qcs,
+                              const void * qh, int m, int P, const int8_t * k8,
+                              const float * ksc, int kstride, const void * kc,
+                              const void * vc, int near, int sink, float * o,
+                              int8_t * aqs, float * asc, void * work, size_t work_bytes, void * stream) {
     if (m < 0 || P < 0) return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: m %d / P %d negative", m, P);
+    if (work && ((uintptr_t) work % 16 != 0))
+        return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: the workspace must be 16-byte aligned");
     if (m == 0) return 0;
     if (kstride % 4 != 0 || kstride < P + m)
         return lk_fail(hipErrorInvalidValue, "lk_pf_attn8: kstride %d must be a multiple of 4 and >= P+m %d", kstride, P + m);
@@ -1423,9 +1486,18 @@ extern "C" int lk_pf_attn8_q81(const int8_t * q8, const float * qsc, const float
     auto go = [&](auto launch) {
         return launch(q8, qsc, qcs, (const _Float16 *) qh, m, P, k8, ksc, kstride,
                       (const _Float16 *) kc, (const _Float16 *) vc, near, sink, o,
-                      aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn8");
+                      aqs, (float2 *) asc, (float *) work, work_bytes, lk_stream(stream), "lk_pf_attn8");
     };
     return aqs ? go(pf_attn_launch<true, true>) : go(pf_attn_launch<true, false>);
+}
+
+extern "C" int lk_pf_attn8_q81(const int8_t * q8, const float * qsc, const float * qcs,
+                               const void * qh, int m, int P, const int8_t * k8,
+                               const float * ksc, int kstride, const void * kc,
+                               const void * vc, int near, int sink, float * o,
+                               int8_t * aqs, float * asc, void * stream) {
+    return lk_pf_attn8_ws(q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc,
+                          nullptr, 0, stream);
 }
 
 extern "C" int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * qcs,
@@ -1437,18 +1509,26 @@ extern "C" int lk_pf_attn8(const int8_t * q8, const float * qsc, const float * q
                            nullptr, nullptr, stream);
 }
 
-extern "C" int lk_pf_attn_q81(const void * qh, int m, int P, const void * kc, const void * vc,
-                              float * o, int8_t * aqs, float * asc, void * stream) {
+extern "C" int lk_pf_attn_ws(const void * qh, int m, int P, const void * kc, const void * vc,
+                             float * o, int8_t * aqs, float * asc, void * work, size_t work_bytes,
+                             void * stream) {
     if (m < 0 || P < 0) return lk_fail(hipErrorInvalidValue, "lk_pf_attn: m %d / P %d negative", m, P);
+    if (work && ((uintptr_t) work % 16 != 0))
+        return lk_fail(hipErrorInvalidValue, "lk_pf_attn: the workspace must be 16-byte aligned");
     if (m == 0) return 0;
     if (!qh || !kc || !vc || (!o && !aqs) || (!aqs != !asc))
         return lk_fail(hipErrorInvalidValue, "lk_pf_attn: null pointer argument");
     auto go = [&](auto launch) {
         return launch(nullptr, nullptr, nullptr, (const _Float16 *) qh, m, P, nullptr, nullptr, 0,
                       (const _Float16 *) kc, (const _Float16 *) vc, 0, 0, o,
-                      aqs, (float2 *) asc, lk_stream(stream), "lk_pf_attn");
+                      aqs, (float2 *) asc, (float *) work, work_bytes, lk_stream(stream), "lk_pf_attn");
     };
     return aqs ? go(pf_attn_launch<false, true>) : go(pf_attn_launch<false, false>);
+}
+
+extern "C" int lk_pf_attn_q81(const void * qh, int m, int P, const void * kc, const void * vc,
+                              float * o, int8_t * aqs, float * asc, void * stream) {
+    return lk_pf_attn_ws(qh, m, P, kc, vc, o, aqs, asc, nullptr, 0, stream);
 }
 
 extern "C" int lk_pf_attn(const void * qh, int m, int P, const void * kc, const void * vc,

@@ -34,6 +34,7 @@ EXPORTS = (
     "lk_pf_ctx_create", "lk_pf_ctx_destroy", "lk_pf_chunk_attn", "lk_pf_chunk_done", "lk_pf_ctx_buffers",
     "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows", "lk_gemv_q4_0", "lk_pf_gemm_q4_0",
     "lk_attn_decode_noalloc", "lk_rope_freq_table",
+    "lk_pf_part_bytes", "lk_pf_attn8_ws", "lk_pf_attn_ws", "lk_pf_gsync_limit", "lk_pf_gsync_faults",
 )
 
 
@@ -97,6 +98,11 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_quant_rows": ([P, I, I, I, P, P, P], I),
         "lk_pf_chunk_done": ([P, I], I),
         "lk_pf_ctx_buffers": ([P, I, P, P, P, P, P, P], I),
+        "lk_pf_part_bytes": ([], S),
+        "lk_pf_attn8_ws": ([P, P, P, P, I, I, P, P, I, P, P, I, I, P, P, P, P, S, P], I),
+        "lk_pf_attn_ws": ([P, I, I, P, P, P, P, P, P, S, P], I),
+        "lk_pf_gsync_limit": ([I], I),
+        "lk_pf_gsync_faults": ([P, I], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -309,6 +315,41 @@ def pf_attn8_q81(q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o
 def pf_attn_q81(qh, m, P, kc, vc, o, aqs, asc, stream=None) -> None:
     _check(load().lk_pf_attn_q81(_ptr(qh), int(m), int(P), _ptr(kc), _ptr(vc), _ptr(o), _ptr(aqs), _ptr(asc),
                                  _stream(stream)), "lk_pf_attn_q81")
+
+
+def pf_part_bytes() -> int:
+    """Bytes of the largest split-K partial workspace a prefill launch uses."""
+    return int(load().lk_pf_part_bytes())
+
+
+def _nbytes(t) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
+
+
+def pf_attn8_ws(q8, qsc, qcs, qh, m, P, k8, ksc, kstride, kc, vc, near, sink, o, aqs, asc, work,
+                stream=None) -> None:
+    """pf_attn8_q81 with a caller-owned split-K workspace (a device tensor; None:
+    the library's static scratch)."""
+    _check(load().lk_pf_attn8_ws(_ptr(q8), _ptr(qsc), _ptr(qcs), _ptr(qh), int(m), int(P), _ptr(k8), _ptr(ksc),
+                                 int(kstride), _ptr(kc), _ptr(vc), int(near), int(sink), _ptr(o), _ptr(aqs),
+                                 _ptr(asc), _ptr(work), _nbytes(work), _stream(stream)), "lk_pf_attn8_ws")
+
+
+def pf_attn_ws(qh, m, P, kc, vc, o, aqs, asc, work, stream=None) -> None:
+    _check(load().lk_pf_attn_ws(_ptr(qh), int(m), int(P), _ptr(kc), _ptr(vc), _ptr(o), _ptr(aqs), _ptr(asc),
+                                _ptr(work), _nbytes(work), _stream(stream)), "lk_pf_attn_ws")
+
+
+def pf_gsync_limit(polls: int) -> None:
+    """Poll bound of the paired prefill kernel's group barriers (0: default)."""
+    _check(load().lk_pf_gsync_limit(int(polls)), "lk_pf_gsync_limit")
+
+
+def pf_gsync_faults(reset: bool = False) -> int:
+    """Group barriers that gave up on this device since the last reset (synchronous)."""
+    c = ctypes.c_uint()
+    _check(load().lk_pf_gsync_faults(ctypes.byref(c), int(bool(reset))), "lk_pf_gsync_faults")
+    return c.value
 
 
 def pf_quant_rows(X, rows, ld, kb, qs, sc, stream=None) -> None:

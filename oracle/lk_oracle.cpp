@@ -19,6 +19,7 @@
 #include <vector>
 #include <random>
 #include <algorithm>
+#include <omp.h>
 
 #define LKO_H   32
 #define LKO_KV  8
@@ -95,9 +96,11 @@ void lko_attn_slices(int seq, int split_cap, int target_n, int split_min,
 // the fp16 cache kc/vc [.][8][64].  q: fp32 [32][64].  out: double [32][64].
 void lko_decode_ref(const float * q, const uint16_t * kc, const uint16_t * vc,
                     int seq, double * out) {
-    std::vector<double> s(seq > 0 ? seq : 1);
-    std::vector<double> kf(LKO_D);
+    // heads are independent: one per OpenMP iteration, each with its own score
+    // row (the result does not depend on the thread count)
+#pragma omp parallel for schedule(static)
     for (int head = 0; head < LKO_H; ++head) {
+        std::vector<double> s(seq > 0 ? seq : 1);
         const int kv = head / LKO_G;
         double m = -1e300;
         for (int t = 0; t < seq; ++t) {
@@ -251,11 +254,14 @@ int lko_pf_exact(int P, int qt, int kt, int near, int sink) {
 void lko_pf_ref(const uint16_t * qh, int m, int P, const uint16_t * kc, const uint16_t * vc,
                 const int * rows, int nrows, double * o) {
     const int S = P + m;
-    std::vector<double> sc(S), qd(LKO_D);
     const int nr = rows ? nrows : m;
-    for (int ri = 0; ri < nr; ++ri) {
+    // (row, head) pairs are independent: one per OpenMP iteration
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long it = 0; it < (long) nr * LKO_H; ++it) {
+        std::vector<double> sc(S), qd(LKO_D);
+        const int ri = (int) (it / LKO_H), h = (int) (it % LKO_H);
         const int t = rows ? rows[ri] : ri;
-        for (int h = 0; h < LKO_H; ++h) {
+        {
             const int kvh = h / LKO_G, qp = P + t;
             for (int d = 0; d < LKO_D; ++d) qd[d] = lko_h2f(qh[(size_t) t * 2048 + h * 64 + d]);
             double mx = -1e300;
@@ -292,12 +298,15 @@ void lko_pf_ref8(const int8_t * q8, const float * qsc, const float * qcs, const 
                  const uint16_t * kc, const uint16_t * vc, int near, int sink,
                  const int * rows, int nrows, double * o) {
     const int S = P + m;
-    std::vector<double> sc(S), qd(LKO_D);
     const int nr = rows ? nrows : m;
-    for (int ri = 0; ri < nr; ++ri) {
+    // (row, head) pairs are independent: one per OpenMP iteration
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long it = 0; it < (long) nr * LKO_H; ++it) {
+        std::vector<double> sc(S), qd(LKO_D);
+        const int ri = (int) (it / LKO_H), h = (int) (it % LKO_H);
         const int t = rows ? rows[ri] : ri;
         const int qt = t / 32;
-        for (int h = 0; h < LKO_H; ++h) {
+        {
             const int kvh = h / LKO_G, qp = P + t;
             for (int d = 0; d < LKO_D; ++d) qd[d] = lko_h2f(qh[(size_t) t * 2048 + h * 64 + d]);
             const int8_t * qi = q8 + (size_t) t * 2048 + h * 64;
@@ -328,6 +337,13 @@ void lko_pf_ref8(const int8_t * q8, const float * qsc, const float * qcs, const 
             }
         }
     }
+}
+
+// Threads of the float64 references (decode_ref, pf_ref, pf_ref8); n <= 0
+// leaves OpenMP's default (OMP_NUM_THREADS).  Returns the count in effect.
+int lko_set_threads(int n) {
+    if (n > 0) omp_set_num_threads(n);
+    return omp_get_max_threads();
 }
 
 // Raw int32 Q.K^T sums: s[h][i][j] = sum_d q8[i][h][d] * k8[j][h/4][d].

@@ -62,6 +62,7 @@ def load():
         "lko_dot_q4_0_q8_1": ([P, ctypes.c_uint16, P], F),
         "lko_gemv_q4_0": ([P, P, P, I, I, P, F, P, I], None),
         "lko_pf_gemm_q4_0": ([P, P, I, I, P, P, I, P, P, I, I], None),
+        "lko_set_threads": ([I], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -69,6 +70,11 @@ def load():
         fn.restype = res
     _lib = lib
     return lib
+
+
+def set_threads(n: int = 0) -> int:
+    """Threads of the float64 references (0: OpenMP's default); returns the count in effect."""
+    return int(load().lko_set_threads(int(n)))
 
 
 def _p(a):

@@ -131,6 +131,26 @@ def test_host_argument_errors():
     assert lib.lk_pf_gemm_q4_0(None, None, 128, 64, None, None, 0, None, None, 128, 0, None) == 0  # no tokens
     assert lib.lk_pf_gemm_q4_0(p, p, 128, 2048, p, p, 65536, None, p, 128, 0, None) == 1  # 4 GiB of activations
     assert b"4 GiB" in lib.lk_last_error()
+    # the decode split reads q with 16-byte loads: every entry point that runs it checks q
+    assert lib.lk_attn_split(q, p, p, p, p, None) == 1
+    assert b"16-byte" in lib.lk_last_error()
+    assert lib.lk_attn_decode(q, p, p, p, p, p, None, None) == 1
+    assert b"16-byte" in lib.lk_last_error()
+    assert lib.lk_attn_decode_noalloc(q, p, p, p, p, None, None) == 1
+    assert b"16-byte" in lib.lk_last_error()
+    assert lib.lk_decode_graph_create(1, ctypes.byref(q), ctypes.byref(p), ctypes.byref(p), p, p, None, None,
+                                      p, ctypes.byref(h)) == 1
+    assert b"16-byte" in lib.lk_last_error()
+    # prefill workspaces are 16-byte aligned; their size is the static scratch's
+    S = ctypes.c_size_t
+    assert lib.lk_pf_attn8_ws(p, p, p, p, 4, 0, p, p, 8, p, p, 0, 0, p, None, None, q, S(4096), None) == 1
+    assert b"workspace" in lib.lk_last_error()
+    assert lib.lk_pf_attn_ws(p, 4, 0, p, p, p, None, None, q, S(4096), None) == 1
+    assert lib.lk_pf_attn_ws(None, 0, 0, None, None, None, None, None, None, S(0), None) == 0
+    assert lib.lk_pf_part_bytes() == 64 << 20
+    assert lib.lk_pf_gsync_limit(-1) == 1
+    assert lib.lk_pf_gsync_limit(0) == 0
+    assert lib.lk_pf_gsync_faults(None, 0) == 1
 
 
 def test_python_mirror_fails_loudly_without_library(tmp_path):

@@ -105,13 +105,24 @@ def test_qk_int32_bit_exact(lk, oracle):
     m, n = 48, 80
     q8 = rng.integers(-127, 128, (m, 2048)).astype(np.int8)
     k8 = rng.integers(-127, 128, (n, 8, 64)).astype(np.int8)
-    k8[0, :, :] = -127                                         # extreme sums
-    q8[0, :] = -127
+    # extreme sums: the kernel reads the MFMA result as the fp32 1.5 * 2^23 + sum,
+    # exact while |sum| < 2^22; int8 operands reach at most 64 * 128 * 128 = 2^20
+    k8[0, :, :] = -127; q8[0, :] = -127                        # +1032256 (quantiser range)
+    k8[1, :, :] = -128; q8[1, :] = -128                        # +2^20, the int8 maximum
+    q8[2, :] = 127                                             # 127 * -128 * 64 = -1040384
+    k8[3, :, :] = 127; q8[3, :] = -128                         # -1040384 again, other operand
+    k8[4, :, :] = 1                                            # sums near 0, both signs
+    q8[4, :] = np.tile(np.array([1, -1], np.int8), 1024)
     s = torch.zeros(32, m, n, dtype=torch.int32, device="cuda")
     note("pf int32 QK^T")
     lk.pf_qk_i32(dev(q8), m, dev(k8), n, s)
     torch.cuda.synchronize()
-    assert np.array_equal(host(s), oracle.qk_i32(q8, m, k8, n))
+    ref = oracle.qk_i32(q8, m, k8, n)
+    assert ref.max() == 1 << 20 and ref.min() == -1040384     # the extremes are exercised
+    got = host(s)
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, (f"{len(bad)} sums differ, first {bad[:8].tolist()}: "
+                           f"got {[int(got[tuple(i)]) for i in bad[:8]]} want {[int(ref[tuple(i)]) for i in bad[:8]]}")
 
 
 # ---- fp16 kernel ---------------------------------------------------------------------------
@@ -315,7 +326,8 @@ def test_attn_auto_split(lk, oracle, m, P, near):
 # ---- BASELINE prefill configurations (sampled rows against the float64 oracle) -----------------
 def _config_rows(m, long_ctx):
     if long_ctx:
-        rows = {0, 63, 64, 1023, 2048, m - 1}
+        # every 64-row block edge, and the middle of the chunk
+        rows = {r for b in range(0, m, 64) for r in (b, b + 63) if r < m} | {1023, 2048}
     else:
         # every 64-row block boundary (the kernel's query blocks, and so the
         # split-K parts' edges), the 32-row exactness tiles around the window
@@ -391,11 +403,53 @@ def test_config_c5_chunk(lk, oracle, P):
     qh, kc, vc, S = lk_configs.prefill_inputs("C5")
     err = _config_check(lk, oracle, qh, kc, vc, P, 4096, 1024, 1, pure_rows=[0, 1000, 2047, 3000, 4095])
     assert err["fp16"][1] <= 2e-3
-    # int8 on these rows: about 0.1 rel-RMS (the x20 channels set every row's
-    # absmax scale, so the other 62 channels keep 1-3 int8 levels).  That is the
-    # reference algorithm's own error (the same-algorithm check above holds to
-    # 2e-3); the bound only catches a blow-up.
-    assert err["int8"][0] <= 0.3 and err["int8"][1] <= 2.0
+    # int8 on these rows, measured on MI355X: rel-RMS 0.101 / max-rel 0.85 at
+    # P = 65536, 0.099 / 0.785 at P = 126976.  The x20 channels set every row's
+    # absmax scale, so the other 62 channels keep 1-3 int8 levels: this is the
+    # reference algorithm's own error on outlier channels (the same-algorithm
+    # check above holds it to 2e-3), bounded about 25% above the measurement so
+    # that a regression shows.
+    assert err["int8"][0] <= 0.125 and err["int8"][1] <= 1.0
+
+
+def test_config_c5_every_chunk(lk, oracle):
+    """All 32 chunks of the C5 prompt as bench.py runs them (the int8 K copy
+    extended chunk by chunk, Q quantised inside the attention kernel, the
+    automatic launch choice: paired, split or unsplit), each checked on
+    sampled rows against the float64 restatement of the same int8 algorithm
+    (2e-3).  The rows move with the chunk: its first and last row, two 64-row
+    block edges and one seeded row."""
+    import lk_configs
+    note("prefill config C5, all 32 chunks of 4096 (sampled rows)")
+    qh, kc, vc, S = lk_configs.prefill_inputs("C5")
+    m = 4096
+    ks = lk.kstride_for(S)
+    k8 = torch.empty(S * 512, dtype=torch.int8, device="cuda")
+    ksc = torch.empty(8 * ks + 4, device="cuda")
+    o = torch.empty(m, 2048, device="cuda")
+    rng = np.random.default_rng(55)
+    outs, rows_of = {}, {}
+    for c, P in enumerate(range(0, S, m)):
+        lk.pf_k8(kc, P, P + m, None, ks, k8, ksc)
+        qchunk = qh[P:P + m].contiguous()
+        lk.pf_attn8(None, None, None, qchunk, m, P, k8, ksc, ks, kc, vc, 1024, 1, o)
+        b = 64 * ((c * 7) % 63)
+        rows = np.array(sorted({0, b + 63, b + 64, int(rng.integers(0, m)), m - 1}), np.int32)
+        rows_of[P] = rows
+        outs[P] = host(o)[rows]
+    torch.cuda.synchronize()
+    Kh, Vh = host_h(kc).reshape(-1), host_h(vc).reshape(-1)
+    K8, KSC = host(k8), host(ksc)
+    Qall = host_h(qh)
+    worst = 0.0
+    for P, rows in rows_of.items():
+        Qc = np.ascontiguousarray(Qall[P:P + m])
+        q8, qsc, qcs = oracle.pf_q8(Qc, m)
+        ref8 = oracle.pf_ref8(q8, qsc, qcs, Qc, m, P, K8, KSC, ks, Kh, Vh, 1024, 1, rows=rows)[rows]
+        rel = oracle.rel_err(outs[P], ref8)
+        worst = max(worst, rel)
+        assert rel <= 2e-3, f"chunk at P={P}: rel {rel:.3e} on rows {rows.tolist()}"
+    note(f"  worst chunk rel vs same-algorithm float64: {worst:.3e}")
 
 
 # ---- planar Q8_1 of the attention output (reference k_pf_quant_rows) ----------------------------

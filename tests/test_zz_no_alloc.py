@@ -55,3 +55,32 @@ def test_no_alloc_matches_workspace_entry(lk, oracle):
 def test_no_alloc_rejects_null(lk):
     rc = lk.load().lk_attn_decode_noalloc(None, None, None, None, None, None, None)
     assert rc == 1 and b"null" in lk.load().lk_last_error()
+
+
+def test_no_alloc_refuses_a_second_stream_while_pending(lk):
+    """Every call on a GPU shares its static array: a call on stream B while one
+    on stream A is still pending is refused with hipErrorNotReady (600) and a
+    message; calls ordered on one stream are accepted, and so is B once A has
+    completed.  A's result is intact."""
+    seq = 4096
+    q, kc, vc = _inputs(seq, 9)
+    qd, kd, vd = dev(q), dev_h(kc), dev_h(vc)
+    o_ref, _ = _with_part(lk, qd, kd, vd, seq)
+    pos = d_pos_for(seq)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    oa = torch.full((32, 64), float("nan"), device="cuda")
+    ob = torch.full((32, 64), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    note("lk_attn_decode_noalloc: guard of the shared array across two streams")
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(200_000_000)              # keep stream A busy (about 0.1 s)
+    lk.attn_decode_noalloc(qd, kd, vd, pos, oa, None, stream=sa)
+    lk.attn_decode_noalloc(qd, kd, vd, pos, oa, None, stream=sa)    # same stream: accepted
+    with pytest.raises(lk.LkError) as ei:
+        lk.attn_decode_noalloc(qd, kd, vd, pos, ob, None, stream=sb)
+    assert "hipError 600" in str(ei.value) and "another stream" in str(ei.value)
+    sa.synchronize()
+    lk.attn_decode_noalloc(qd, kd, vd, pos, ob, None, stream=sb)    # A is done: accepted
+    sb.synchronize()
+    assert np.array_equal(host(oa).view(np.uint32), o_ref.view(np.uint32))
+    assert np.array_equal(host(ob).view(np.uint32), o_ref.view(np.uint32))
