@@ -31,16 +31,40 @@ PEAK_FP16_TFLOPS = 2500.0             # dense fp16 MFMA
 REF_3090TI_GBS_32K = 669.3            # reference, RTX 3090 Ti, docs/ARCHITECTURE.md:2401
 
 
+DECODE_SOURCES = ("lfm2-ampere_amd/csrc/decode.hip", "lfm2-ampere_amd/csrc/lk_common.h",
+                  "lfm2-ampere_amd/Makefile")
+
+
+def decode_source_sha16():
+    """sha256 (first 16 hex digits) over the sources the split kernel is built
+    from; a committed counter profile records the value it was taken on."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in DECODE_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def split_traffic_from_profile():
-    """HBM bytes per C2 split launch, from the committed rocprofv3 FETCH_SIZE +
-    WRITE_SIZE summary (calibrated against a 1 GiB copy), or None."""
+    """HBM bytes per C2 split launch from the committed rocprofv3 FETCH_SIZE +
+    WRITE_SIZE summary (calibrated against a 1 GiB copy) -- a counter figure
+    that needs its own profiler runs, so it is read from the profile, not
+    measured here -- and only when that profile was taken on these very
+    sources: returns (bytes or None, note)."""
     import re
     try:
         txt = open(os.path.join(ROOT, "profiles", "decode_attn_c2_c3.md")).read()
     except OSError:
-        return None
+        return None, "no profile"
     m = re.search(r"traffic_bytes_per_launch = (\d+)", txt)
-    return int(m.group(1)) if m else None
+    s = re.search(r"source_sha16 = ([0-9a-f]{16})", txt)
+    if not m:
+        return None, "no traffic figure in profiles/decode_attn_c2_c3.md"
+    cur = decode_source_sha16()
+    if not s or s.group(1) != cur:
+        return None, f"profiles/decode_attn_c2_c3.md is stale (taken on sources {s.group(1) if s else '?'}, now {cur})"
+    return int(m.group(1)), f"from profiles/decode_attn_c2_c3.md, taken on sources {cur} (these)"
 
 
 def log(msg):
@@ -74,9 +98,9 @@ def spread_us(t):
             "reps": t["reps"], "iters": t["iters"]}
 
 
-def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters):
+def bench_decode(lk, lkc, cfg, steps, warmup, kernel_iters, seq=None):
     import torch
-    qs, kcs, vcs, seq = lkc.decode_inputs(cfg, layers=10)
+    qs, kcs, vcs, seq = lkc.decode_inputs(cfg, layers=10, seq=seq)
     layers = len(qs)
     d_pos = torch.tensor([seq - 1], dtype=torch.int32, device="cuda")
     part = torch.empty(lk.part_bytes() // 4, device="cuda")
@@ -319,6 +343,42 @@ def bench_prefill_c5(lk, lkc, reps):
     }, samples
 
 
+def bench_decode_curve(lk, lkc, c2, c3, steps, warmup, kernel_iters, extra=(8192, 65536)):
+    """Decode attention per layer over context length -- the reference's own
+    curve is 8192, 32768, 65536 and 131040 (docs/ARCHITECTURE.md:2400-2403)
+    with the fixed-cost model 23.3 us + bytes / 856 GB/s (:2411).  The 8k and
+    65k points are measured here (10-layer graphs, C2's distributions); 32k and
+    131k are C2 and C3.  The same model is fitted by least squares to the
+    layer times and, separately, to the split kernel's own times."""
+    pts = []
+    for seq in extra:
+        r = bench_decode(lk, lkc, "C2", steps, warmup, kernel_iters, seq=seq)
+        pts.append(r)
+    pts += [c2, c3]
+    pts.sort(key=lambda r: r["seq"])
+
+    def fit(key):
+        xs = [r["seq"] * 2048.0 for r in pts]
+        ys = [r[key] for r in pts]
+        n = len(xs)
+        mx, my = sum(xs) / n, sum(ys) / n
+        sxx = sum((x - mx) ** 2 for x in xs)
+        sxy = sum((x - mx) * (y - my) for x, y in zip(xs, ys))
+        slope = sxy / sxx                              # us per byte
+        a = my - slope * mx
+        resid = max(abs(y - (a + slope * x)) for x, y in zip(xs, ys))
+        return {"fixed_us": a, "GBps": 1e-3 / slope, "max_residual_us": resid}
+
+    return {
+        "points": [{"seq": r["seq"], "us_per_layer": r["us_per_layer"], "GBps": r["GBps"],
+                    "split_us": r["split_us"], "combine_us": r["combine_us"],
+                    "layer_frac": r["layer_frac"]} for r in pts],
+        "fit_layer": fit("us_per_layer"),
+        "fit_split": fit("split_us"),
+        "reference_fit": {"fixed_us": 23.3, "GBps": 856.0, "hardware": "RTX 3090 Ti"},
+    }
+
+
 def bench_read_reference(lk, bytes_list=(67108864, 268435456), nbuf=10, iters=20):
     """The practical HBM read rate of this GPU, for scale: the library's plain
     streaming-read probe (lk_read_probe) over buffers of the decode layers'
@@ -509,12 +569,15 @@ def bench_pf_driver(lk, n_tok=32768, chunks=(4096, 8192)):
     return {"prompt_tokens": n_tok, "layers": 1, **res}
 
 
-def cpu_baseline(seconds, prefill=True, c5_samples=None):
+def cpu_baseline(seconds, prefill=True, c5_samples=None, c4_full_1t=False):
     """The reference's CPU path restated in the oracle (float64, single
     thread): decode attention (tests/test_attn.cu:46-74) on a full C2 layer and
     on C1, and prefill attention (tests/test_prefill.cu:263-282) on sampled
     query rows of C4 and of C5's last chunk, extrapolated by the number of
-    (query, key) pairs to the whole chunk / prompt.
+    (query, key) pairs to the whole chunk / prompt.  Beside them, the whole C4
+    chunk (every row and head, no extrapolation) timed once with OpenMP over
+    (row, head) on all the host threads OpenMP is given, the thread count
+    stated; with c4_full_1t also the whole C4 chunk on one thread (about 80 s).
 
     With c5_samples (the GPU kernels' outputs on sampled rows of C5 chunks),
     the float64 attention of those rows is also the checker of the int8 and
@@ -527,6 +590,7 @@ def cpu_baseline(seconds, prefill=True, c5_samples=None):
     import lk_oracle as orc
     import lk_configs as lkc
     res = {}
+    orc.set_threads(1)
     for cfg, budget in (("C2", seconds), ("C1", max(2.0, seconds / 5))):
         qs, kcs, vcs, seq = lkc.decode_inputs(cfg, layers=1)
         q = qs[0].cpu().numpy()
@@ -576,6 +640,19 @@ def cpu_baseline(seconds, prefill=True, c5_samples=None):
                                      "max_rel": float(np.max(np.abs(e)) / np.max(np.abs(ref)))}
                 acc[f"P{P0}"] = ent
             res["C5_accuracy"] = acc
+        if cfg == "C4":
+            # OpenMP's default thread count is OMP_NUM_THREADS (the box's CPU share)
+            omp_default = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+            runs = [("C4_full_1thread", 1)] if c4_full_1t else []
+            runs.append(("C4_full_openmp", omp_default))
+            for key, th in runs:
+                nth = orc.set_threads(th)
+                t0 = time.perf_counter()
+                orc.pf_ref(Q, m, P, K, V)
+                dt = time.perf_counter() - t0
+                res[key] = {"s": dt, "TOPS": pairs_full * 256.0 / dt / 1e12, "threads": nth,
+                            "note": "float64 reference over the whole C4 chunk (all 4096 rows, 32 heads)"}
+            orc.set_threads(1)
         del qh, kc, vc
         torch.cuda.empty_cache()
     return res
@@ -635,6 +712,8 @@ def main():
     ap.add_argument("--skip-prefill", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-c4-1thread", action="store_true",
+                    help="also time the whole C4 chunk's float64 reference on one thread (about 80 s)")
     ap.add_argument("--profile-split", type=int, default=0,
                     help="only run N C2 split launches + a 1 GiB copy (for rocprofv3 --pmc)")
     ap.add_argument("--profile-prefill", choices=["c4", "c5"], default=None,
@@ -672,6 +751,10 @@ def main():
     c3 = bench_decode(lk, lkc, "C3", max(20, args.steps // 4), max(3, args.warmup // 4), args.kernel_iters // 2)
     log(json.dumps(c3))
     results = {"C2_decode_32k": c2, "C3_decode_131k": c3}
+    log("decode curve over context length (C2 distributions, 10 layers, one hipGraph)")
+    results["decode_curve"] = bench_decode_curve(lk, lkc, c2, c3, max(20, args.steps // 4), max(3, args.warmup // 4),
+                                                 args.kernel_iters // 2)
+    log(json.dumps(results["decode_curve"]))
     log("practical HBM read rate (plain streaming read of the decode layer sizes)")
     results["hbm_read_reference"] = bench_read_reference(lk)
     log(json.dumps(results["hbm_read_reference"]))
@@ -704,8 +787,9 @@ def main():
 
     cpu = None
     if not args.skip_cpu:
-        log("cpu baseline (float64 oracle, 1 thread)")
-        cb = cpu_baseline(args.cpu_seconds, prefill=not args.skip_prefill, c5_samples=c5_samples)
+        log("cpu baseline (float64 oracle, 1 thread; the whole C4 chunk also over all host threads)")
+        cb = cpu_baseline(args.cpu_seconds, prefill=not args.skip_prefill, c5_samples=c5_samples,
+                          c4_full_1t=args.cpu_c4_1thread)
         if "C5_accuracy" in cb:
             results["C5_prefill_131k"]["accuracy_vs_float64"] = cb.pop("C5_accuracy")
         results["cpu_float64"] = cb
@@ -716,6 +800,7 @@ def main():
                          f"extrapolated) under results.cpu_float64"}
 
     ach = c2["split_GBps"]
+    traffic, traffic_note = split_traffic_from_profile()
     line = {
         "metric": "decode attn us/layer + HBM GB/s @32k/131k; prefill attn TOPS @4k/131k",
         "value": round(c2["GBps"], 2),
@@ -737,7 +822,8 @@ def main():
             "baseline": "reference on RTX 3090 Ti: 669.3 GB/s, 100.27 us/layer @32768",
         },
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": split_traffic_from_profile(),
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_note,
                      "kernel": "lk_k_attn_split (C2, seq x 2048 B per launch)"},
         "cpu_baseline": cpu,
         "results": results,

@@ -380,6 +380,17 @@ int lk_rope_freq_table(float * out);
  * meets.  No counterpart in the reference. */
 int lk_read_probe(const void * src, size_t bytes, float * sink, void * stream);
 
+/* Measurement utility, not on the attention path: the seeded synthetic inputs
+ * of the benchmark configurations, generated on the device.  n fp32 values of
+ * the splitmix64 stream of `seed` (draw k = mix(seed + k * 0x9e3779b97f4a7c15),
+ * k = 1, 2, ...; u = ((x >> 11) + 1) / 2^53) into out:
+ *   kind 0: N(0,1) by Box-Muller in float64 (pair j: draws 2j+1, 2j+2; cos,
+ *           then sin), kind 1: uniform lo + (hi - lo) * u, kind 2: Student-t
+ *           with nu = 4 (draws 10i+1 .. 10i+10: z / sqrt(chi2_4 / 4)).
+ * The same values as a sequential host generator of the same definition.  No
+ * counterpart in the reference (its CUDA harnesses use their own generators). */
+int lk_synth_f32(int kind, uint64_t seed, size_t n, float lo, float hi, float * out, void * stream);
+
 /* ---- the consumer of the decode attention output ------------------------ */
 
 /* Q4_0 x Q8_1 GEMV: replaces k_gemv_q4_0 (reference kernels.cu:300-306, body

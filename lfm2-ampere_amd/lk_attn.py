@@ -35,6 +35,7 @@ EXPORTS = (
     "lk_pf_attn8_q81", "lk_pf_attn_q81", "lk_pf_quant_rows", "lk_gemv_q4_0", "lk_pf_gemm_q4_0",
     "lk_attn_decode_noalloc", "lk_rope_freq_table",
     "lk_pf_part_bytes", "lk_pf_attn8_ws", "lk_pf_attn_ws", "lk_pf_gsync_limit", "lk_pf_gsync_faults",
+    "lk_synth_f32",
 )
 
 
@@ -103,6 +104,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         "lk_pf_attn_ws": ([P, I, I, P, P, P, P, P, P, S, P], I),
         "lk_pf_gsync_limit": ([I], I),
         "lk_pf_gsync_faults": ([P, I], I),
+        "lk_synth_f32": ([I, ctypes.c_uint64, S, ctypes.c_float, ctypes.c_float, P, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -350,6 +352,18 @@ def pf_gsync_faults(reset: bool = False) -> int:
     c = ctypes.c_uint()
     _check(load().lk_pf_gsync_faults(ctypes.byref(c), int(bool(reset))), "lk_pf_gsync_faults")
     return c.value
+
+
+SYNTH_NORMAL, SYNTH_UNIFORM, SYNTH_STUDENT4 = 0, 1, 2
+
+
+def synth(kind: int, seed: int, out, lo: float = 0.0, hi: float = 1.0, stream=None) -> None:
+    """Fill the fp32 device tensor `out` with the seeded splitmix64 stream of
+    `seed` (kind: SYNTH_NORMAL, SYNTH_UNIFORM in [lo, hi), SYNTH_STUDENT4)."""
+    if out.dtype != __import__("torch").float32:
+        raise ValueError("synth: out must be fp32")
+    _check(load().lk_synth_f32(int(kind), int(seed) & ((1 << 64) - 1), out.numel(), float(lo), float(hi),
+                               _ptr(out), _stream(stream)), "lk_synth_f32")
 
 
 def pf_quant_rows(X, rows, ld, kb, qs, sc, stream=None) -> None:

@@ -392,6 +392,12 @@ static inline uint64_t lko_sm64(uint64_t & x) {
 static inline double lko_u01(uint64_t & x) {            // (0, 1]
     return ((double)(lko_sm64(x) >> 11) + 1.0) / 9007199254740992.0;
 }
+// The raw stream: out[k] = draw k + 1 (known answers: seed 1234567 gives
+// 6457827717110365317, 3203168211198807973, 9817491932198370423, ...).
+void lko_sm64_n(uint64_t seed, uint64_t * out, size_t n) {
+    uint64_t x = seed;
+    for (size_t i = 0; i < n; ++i) out[i] = lko_sm64(x);
+}
 // n values N(0,1) in fp32 (Box-Muller, both outputs used).
 void lko_sm_normal(uint64_t seed, float * out, size_t n) {
     uint64_t x = seed;

@@ -63,6 +63,7 @@ def load():
         "lko_gemv_q4_0": ([P, P, P, I, I, P, F, P, I], None),
         "lko_pf_gemm_q4_0": ([P, P, I, I, P, P, I, P, P, I, I], None),
         "lko_set_threads": ([I], I),
+        "lko_sm64_n": ([U64, P, S], None),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -257,6 +258,13 @@ class XorShiftAttnCases:
         vc = np.empty(cache_elems, np.uint16)
         load().lko_xs_fill_attn_case(ctypes.byref(self.state), cache_elems, _p(q), _p(kc), _p(vc))
         return q, kc, vc
+
+
+def sm64(seed: int, n: int) -> np.ndarray:
+    """The first n outputs of the splitmix64 stream of `seed`."""
+    out = np.empty(n, np.uint64)
+    load().lko_sm64_n(seed, _p(out), n)
+    return out
 
 
 def sm_normal(seed: int, n: int) -> np.ndarray:

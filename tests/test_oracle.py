@@ -414,6 +414,44 @@ def test_splitmix_normal_stats(oracle):
     assert abs(np.median(np.abs(t)) - 0.7407) < 0.01
 
 
+def test_splitmix64_known_answers(oracle):
+    """The integer stream the benchmark configurations are drawn from is
+    splitmix64; its published test vector (seed 1234567, S. Vigna's
+    splitmix64.c) pins the oracle's generator and the configs' host copy."""
+    import lk_configs
+    want = [6457827717110365317, 3203168211198807973, 9817491932198370423,
+            4593380528125082431, 16408922859458223821]
+    assert oracle.sm64(1234567, 5).tolist() == want
+    assert lk_configs.sm64_draws(1234567, 5) == want
+    seed = lk_configs.seed_of("C5", 0, lk_configs.T_CHAN, 2)
+    assert oracle.sm64(seed, 64).tolist() == lk_configs.sm64_draws(seed, 64)
+
+
+def test_splitmix_box_muller_composition(oracle):
+    """The normal, uniform and Student-t streams are built from the pinned
+    integer stream exactly as documented: u = ((x >> 11) + 1) / 2^53, pair j of
+    the normals from draws 2j+1, 2j+2 (r = sqrt(-2 ln u1); cos, then sin), the
+    uniform from draw i+1, the Student-t element from draws 10i+1 .. 10i+10."""
+    seed, n = 987654321, 1001
+    x = oracle.sm64(seed, 10 * n + 2)
+    u = ((x >> np.uint64(11)).astype(np.float64) + 1.0) / 9007199254740992.0
+    r = np.sqrt(-2.0 * np.log(u[0::2]))
+    th = 2.0 * np.pi * u[1::2]
+    want = np.empty(2 * len(th), np.float32)
+    want[0::2] = (r * np.cos(th)).astype(np.float32)
+    want[1::2] = (r * np.sin(th)).astype(np.float32)
+    got = oracle.sm_normal(seed, n)
+    assert np.mean(got == want[:n]) > 0.9999 and np.allclose(got, want[:n], rtol=1e-6, atol=1e-7)
+    lo, hi = np.float32(0.5), np.float32(2.0)
+    wu = lo + (hi - lo) * u[:n].astype(np.float32)
+    assert np.array_equal(oracle.sm_uniform(seed, n, 0.5, 2.0), wu)
+    g = np.sqrt(-2.0 * np.log(u[0:10 * n:2])) * np.cos(2.0 * np.pi * u[1:10 * n:2])
+    g = g.reshape(n, 5)
+    wt = (g[:, 0] / np.sqrt((g[:, 1] ** 2 + g[:, 2] ** 2 + g[:, 3] ** 2 + g[:, 4] ** 2) / 4.0)).astype(np.float32)
+    gt = oracle.sm_student4(seed, n)
+    assert np.mean(gt == wt) > 0.999 and np.allclose(gt, wt, rtol=1e-6, atol=1e-7)
+
+
 def test_rel_err_metric(oracle):
     a = np.array([1.0, 2.0, 3.5])
     b = np.array([1.0, 2.0, 4.0])

@@ -391,6 +391,12 @@ def test_config_c4(lk, oracle):
     _config_check(lk, oracle, qh, kc, vc, 0, S, 1024, 1)
 
 
+# int8 against plain float64 on the sampled rows, measured on MI355X with the
+# seeded splitmix64 inputs: (rel-RMS, max-rel) = (0.107, 1.14) at P = 65536 and
+# (0.037, 0.29) at P = 126976.  Bounds sit 25% above, so a regression shows.
+C5_INT8_BOUND = {65536: (0.135, 1.45), 126976: (0.046, 0.36)}
+
+
 @pytest.mark.parametrize("P", [65536, 126976], ids=["mid_chunk", "last_chunk"])
 def test_config_c5_chunk(lk, oracle, P):
     """C5 (heavy-tailed Q/K with x20 outlier channels, the stress case of the
@@ -403,13 +409,11 @@ def test_config_c5_chunk(lk, oracle, P):
     qh, kc, vc, S = lk_configs.prefill_inputs("C5")
     err = _config_check(lk, oracle, qh, kc, vc, P, 4096, 1024, 1, pure_rows=[0, 1000, 2047, 3000, 4095])
     assert err["fp16"][1] <= 2e-3
-    # int8 on these rows, measured on MI355X: rel-RMS 0.101 / max-rel 0.85 at
-    # P = 65536, 0.099 / 0.785 at P = 126976.  The x20 channels set every row's
-    # absmax scale, so the other 62 channels keep 1-3 int8 levels: this is the
-    # reference algorithm's own error on outlier channels (the same-algorithm
-    # check above holds it to 2e-3), bounded about 25% above the measurement so
-    # that a regression shows.
-    assert err["int8"][0] <= 0.125 and err["int8"][1] <= 1.0
+    # The x20 channels set every row's absmax scale, so the other 62 channels
+    # keep 1-3 int8 levels: this is the reference algorithm's own error on
+    # outlier channels (the same-algorithm check above holds it to 2e-3).
+    rms_max, rel_max = C5_INT8_BOUND[P]
+    assert err["int8"][0] <= rms_max and err["int8"][1] <= rel_max
 
 
 def test_config_c5_every_chunk(lk, oracle):
