@@ -603,7 +603,10 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 exa[qb] = LK_LOG2E_F * isq;
                 exb[qb] = -qc * isq;
             } else {
-                qf8[qb] = zi; sq[qb] = 1.0f; exa[qb] = LK_LOG2E_F; exb[qb] = 0.0f;
+                // every tile exact: scores stay the raw fp32 sums (natural-log
+                // units) and log2(e) is the exponent's scale, so the exponent
+                // argument is one fma of the raw sum
+                qf8[qb] = zi; sq[qb] = LK_LOG2E_F; exa[qb] = 1.0f; exb[qb] = 0.0f;
             }
         }
         if (fill_s_q && !fuse_q) fill_sq(qv16);
@@ -714,7 +717,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qa[j][1], c, 0, 0, 0);
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
-                            x[kb][j][i] = fmaf(c[i], exa[qb], exb[qb]);
+                            x[kb][j][i] = INT8 ? fmaf(c[i], exa[qb], exb[qb]) : c[i];
                     }
                 }
             } else {
