@@ -14,13 +14,17 @@
 // ---- split-K operating point --------------------------------------------------
 // The reference's rule (kernels.cuh:630-635) with its cap/target retuned for
 // MI355X: 8 kv heads x LK_ATTN_SPLIT workgroups is the fixed, graph-capturable
-// grid; slices = clamp(ceil(seq/TARGET_N), SPLIT_MIN, SPLIT).  Overridable at
-// build time (-D), like the reference's Makefile knobs.
+// grid; slices = clamp(ceil(seq/TARGET_N), SPLIT_MIN, SPLIT).  TARGET_N = 16
+// (one LDS tile per workgroup) gives every one of the 256 CUs a slice from a
+// 4096-position context up; from 4096 positions on the cap decides.  Measured
+// per layer in a 10-layer graph against TARGET_N = 128: 2k 12.05 -> 8.79 us,
+// 8k 12.29 -> 10.40 us, 16k 12.99 -> 11.89 us, 32k unchanged (capped).
+// Overridable at build time (-D), like the reference's Makefile knobs.
 #ifndef LK_ATTN_SPLIT
 #define LK_ATTN_SPLIT      256
 #endif
 #ifndef LK_ATTN_TARGET_N
-#define LK_ATTN_TARGET_N   128
+#define LK_ATTN_TARGET_N   16
 #endif
 #ifndef LK_ATTN_SPLIT_MIN
 #define LK_ATTN_SPLIT_MIN  8

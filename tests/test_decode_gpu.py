@@ -155,7 +155,7 @@ def test_null_outputs_and_q8_only(lk, oracle):
     assert torch.equal(y1, y2)
 
 
-@pytest.mark.parametrize("seq", [1, 9, 17, 1025, 1031])
+@pytest.mark.parametrize("seq", [1, 9, 17, 1025, 1031, 4100])
 def test_dead_slices_write_neutral_records(lk, oracle, seq):
     """Lengths whose slice plan leaves empty slices (seq / ceil(seq / ns) < ns,
     and every slot past ns): the partial buffer starts as NaN everywhere, the

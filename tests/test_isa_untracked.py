@@ -17,7 +17,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "lfm2-ampere_amd")
 HIPCC = "/opt/rocm/bin/hipcc"
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
-         "-packed-fp32-ops", "-DLK_ATTN_SPLIT=256", "-DLK_ATTN_TARGET_N=128", "-DLK_ATTN_SPLIT_MIN=8",
+         "-packed-fp32-ops", "-DLK_ATTN_SPLIT=256", "-DLK_ATTN_TARGET_N=16", "-DLK_ATTN_SPLIT_MIN=8",
          "-DLK_DEC_TILE=16", "-DLK_DEC_NBUF=4", "-DLK_DEC_ABLATE=0"]
 
 
