@@ -651,6 +651,8 @@ static __device__ __align__(256) float scratch[LK_DEC_SCRATCH_FLOATS];
 // (hipErrorNotReady) instead.  Calls on one stream are ordered and always
 // accepted.  Under stream capture nothing is checked or recorded (the graph's
 // own order decides).  Address and event are set up on a device's first call.
+// A call holds g_dec_mu from the check to the record, so that two host
+// threads cannot both pass the check before either has recorded.
 struct LkDecScratchUse {
     float * ptr = nullptr;
     hipStream_t last = nullptr;
@@ -666,6 +668,7 @@ static bool lk_capturing(hipStream_t st) {
     return cs != hipStreamCaptureStatusNone;
 }
 
+// Called with g_dec_mu held.
 static float * lk_dec_scratch_acquire(hipStream_t st, int & err, int & dev_out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -674,7 +677,6 @@ static float * lk_dec_scratch_acquire(hipStream_t st, int & err, int & dev_out) 
                       "lk_attn_decode_noalloc: no usable current device");
         return nullptr;
     }
-    std::lock_guard<std::mutex> lock(g_dec_mu);
     LkDecScratchUse & u = g_dec_use[dev];
     if (!u.ptr) {
         void * p = nullptr;
@@ -708,9 +710,9 @@ static float * lk_dec_scratch_acquire(hipStream_t st, int & err, int & dev_out) 
 }
 
 // After the combine is enqueued on st: mark the array busy until it completes.
+// Called with g_dec_mu held.
 static int lk_dec_scratch_release(hipStream_t st, int dev) {
     if (lk_capturing(st)) return 0;
-    std::lock_guard<std::mutex> lock(g_dec_mu);
     LkDecScratchUse & u = g_dec_use[dev];
     const hipError_t e = hipEventRecord(u.done, st);
     if (e != hipSuccess) return lk_fail((int) e, "lk_attn_decode_noalloc: guard record: %s", hipGetErrorString(e));
@@ -729,6 +731,7 @@ extern "C" int lk_attn_decode_noalloc(const float * q, const void * kc, const vo
     if (lk_q_misaligned(q))
         return lk_fail(hipErrorInvalidValue, "lk_attn_decode_noalloc: q must be 16-byte aligned");
     hipStream_t st = lk_stream(stream);
+    std::lock_guard<std::mutex> lock(g_dec_mu);
     int err = 0, dev = 0;
     float * part = lk_dec_scratch_acquire(st, err, dev);
     if (!part) return err;

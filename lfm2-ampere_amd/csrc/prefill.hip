@@ -216,6 +216,17 @@ struct PfWork {
 // that bring no workspace of their own.
 #define PF_PART_CAP   (16u << 20)                        // floats
 __device__ float g_pf_part[PF_PART_CAP];
+// Measurement builds only (-DPF_TIMING; no launch of the product reads them):
+// per-wave timestamps of the paired kernel (s_memrealtime, 100 MHz) written
+// into the static partial scratch, which paired launches do not use:
+// [workgroup][wave][4] = start, prologue done, tile loop done, end.
+#ifdef PF_TIMING
+#define PF_TSTAMP(k) do { if (PAIR && lane == 0) { \
+        ((unsigned long long *) g_pf_part)[((size_t) blockIdx.x * 8 + w) * 4 + (k) + lane] = \
+            __builtin_amdgcn_s_memrealtime(); } } while (0)
+#else
+#define PF_TSTAMP(k) do { } while (0)
+#endif
 // Group barriers of the paired kernel that gave up waiting (poll bound spent),
 // counted per device; the workgroup's outputs are then NaN.
 __device__ unsigned g_pf_gsync_fault;
@@ -326,12 +337,10 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // then pair a long block with a short one.  Split launches: one work item
     // (block, key range) per workgroup, longest first.
     const int tid  = threadIdx.x;
-#ifdef PF_AGPR
-    asm volatile("; agpr" :: "a"(0));
-#endif
     const int lane = tid & 63;
     const int w    = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col  = lane & 15, g = lane >> 4;
+    PF_TSTAMP(0);
     const int hw   = w & 3, grp = w >> 2;                 // head within the kv head; PAIR group
     int kvh, qt, kt_lo, kt_hi, pslot = -1;
     int bi = 0, bj = 0, nki = 0, nkj = 0, xs = 0;         // PAIR: the two blocks, their tile counts, the cut of bj
@@ -615,6 +624,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     // PAIR: every wave's s_q block (group A reads group B's for bj) and the
     // group counters are in place before any group goes on
     if constexpr (PAIR) __syncthreads();
+    PF_TSTAMP(1);
     int qw = w;                                       // the s_q block exact tiles read
 
     // O^T blocks [dim block][query block]; block 4 multiplies P^T by an
@@ -961,6 +971,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         // ---- group A's part of bj into group B's, through LDS (the tile stages
         // are free now), in the split-partial layout; lane l of wave hw+4 reads
         // exactly what lane l of wave hw wrote.  Fixed order: B's part, then A's.
+        PF_TSTAMP(2);
         __syncthreads();
         float * R = (float *) &st[0];
         lk_f4 * A = (lk_f4 *) R + (size_t) hw * 16 * PF_BQ;
@@ -993,6 +1004,7 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
             }
             emit();
         }
+        PF_TSTAMP(3);
     }
 }
 
@@ -1200,6 +1212,15 @@ extern "C" int lk_pf_gsync_faults(unsigned * count, int reset) {
 
 extern "C" size_t lk_pf_part_bytes(void) { return (size_t) PF_PART_CAP * sizeof(float); }
 
+#ifdef PF_TIMING
+// Measurement builds only: the paired kernel's per-wave timestamps.
+extern "C" int lk_pf_timing_read(unsigned long long * out, size_t n) {
+    const hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(g_pf_part), n * sizeof(unsigned long long), 0,
+                                             hipMemcpyDeviceToHost);
+    return e == hipSuccess ? 0 : lk_fail((int) e, "lk_pf_timing_read: %s", hipGetErrorString(e));
+}
+#endif
+
 // Device address of the partial scratch, per device (looked up once), and the
 // guard of its single-stream use: the stream of the last splitting launch on
 // each device and an event recorded after its combine.  A splitting launch on
@@ -1207,6 +1228,8 @@ extern "C" size_t lk_pf_part_bytes(void) { return (size_t) PF_PART_CAP * sizeof(
 // the earlier launch has not merged yet; it is refused (hipErrorNotReady)
 // instead.  Launches on one stream are ordered and always accepted.  Under
 // stream capture the guard is not applied (the graph's own order decides).
+// A launch holds g_pf_mu from the check to the record (pf_attn_launch), so
+// that two host threads cannot both pass the check before either has recorded.
 struct PfScratchUse {
     float * ptr = nullptr;
     hipStream_t last = nullptr;
@@ -1216,6 +1239,7 @@ struct PfScratchUse {
 static std::mutex g_pf_mu;
 static PfScratchUse g_pf_use[LK_MAX_DEVICES];
 
+// Called with g_pf_mu held.
 static float * pf_part_acquire(hipStream_t st, int & err, int & dev_out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -1223,7 +1247,6 @@ static float * pf_part_acquire(hipStream_t st, int & err, int & dev_out) {
         err = lk_fail(e != hipSuccess ? (int) e : (int) hipErrorInvalidDevice, "prefill: no usable current device");
         return nullptr;
     }
-    std::lock_guard<std::mutex> lock(g_pf_mu);
     PfScratchUse & u = g_pf_use[dev];
     if (!u.ptr) {
         void * p = nullptr;
@@ -1252,11 +1275,11 @@ static float * pf_part_acquire(hipStream_t st, int & err, int & dev_out) {
 }
 
 // After the combine is enqueued on st: mark the scratch busy until it completes.
+// Called with g_pf_mu held.
 static int pf_part_release(hipStream_t st, int dev) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     (void) hipStreamIsCapturing(st, &cs);
     if (cs != hipStreamCaptureStatusNone) return 0;
-    std::lock_guard<std::mutex> lock(g_pf_mu);
     PfScratchUse & u = g_pf_use[dev];
     const hipError_t e = hipEventRecord(u.done, st);
     if (e != hipSuccess) return lk_fail((int) e, "prefill: scratch guard record: %s", hipGetErrorString(e));
@@ -1454,6 +1477,10 @@ static int pf_attn_launch(const int8_t * q8, const float * qsc, const float * qc
                            (float *) nullptr);
         return lk_launch_status(what);
     }
+    // the static scratch: the guard's check, the launches and its record under
+    // one lock (a caller's workspace needs none)
+    std::unique_lock<std::mutex> lock(g_pf_mu, std::defer_lock);
+    if (!work) lock.lock();
     int err = 0, dev = 0;
     float * pbuf = work ? work : pf_part_acquire(st, err, dev);
     if (!pbuf) return err;
