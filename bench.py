@@ -660,8 +660,12 @@ def cpu_baseline(seconds, prefill=True, c5_samples=None, c4_full_1t=False):
 
 def profile_prefill(lk, lkc, which, launches):
     """For rocprofv3 --pmc runs: `launches` int8 prefill attention launches on
-    C4 (the 4096 chunk at P = 0) or on C5's last chunk (P = 126976)."""
+    C4 (the 4096 chunk at P = 0) or on C5's last chunk (P = 126976); c5pair:
+    that chunk in the paired launch (forced), to set the two launch forms
+    side by side on the same tiles."""
     import torch
+    if which == "c5pair":
+        lk.pf_pair_override(1)
     if which == "c4":
         qh, kc, vc, S = lkc.prefill_inputs("C4")
         m, P, qc = S, 0, qh
@@ -677,6 +681,7 @@ def profile_prefill(lk, lkc, which, launches):
     for _ in range(launches):       # Q quantised inside the kernel, as bench_prefill_c4/c5 time it
         lk.pf_attn8(None, None, None, qc, m, P, k8, ksc, ks, kc, vc, 1024, 1, o)
     torch.cuda.synchronize()
+    lk.pf_pair_override(0)
     oi, of, pairs = pf_ops(m, P)
     log(f"profile: {launches} prefill attention launches ({which}, m {m}, P {P}, "
         f"{pairs:.0f} (query, key) pairs, {oi + of:.4g} algorithmic ops each)")
@@ -716,7 +721,7 @@ def main():
                     help="also time the whole C4 chunk's float64 reference on one thread (about 80 s)")
     ap.add_argument("--profile-split", type=int, default=0,
                     help="only run N C2 split launches + a 1 GiB copy (for rocprofv3 --pmc)")
-    ap.add_argument("--profile-prefill", choices=["c4", "c5"], default=None,
+    ap.add_argument("--profile-prefill", choices=["c4", "c5", "c5pair"], default=None,
                     help="only run --profile-launches int8 prefill attention launches (for rocprofv3 --pmc)")
     ap.add_argument("--profile-launches", type=int, default=3)
     ap.add_argument("--profile-gemv", action="store_true",

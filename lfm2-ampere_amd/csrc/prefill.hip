@@ -330,6 +330,10 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     __shared__ PfStage st[PAIR ? 4 : 2];                  // PAIR: [stage][slot]
     __shared__ __attribute__((aligned(16))) int8_t s_q[NW][PF_BQ * PF_Q_LD];  // fp16 Q, per wave
     __shared__ __attribute__((aligned(16))) float s_kp[NW][2 * PF_BK];         // per wave: ks', -PF_MAGIC*ks'
+    // PAIR: each lane's DMA source offsets (int8 K, fp16 K and V rows of key
+    // group 0; all below 2^16), formed once and re-read per issue (see
+    // issue_to).  They depend on the wave's head, not on its group.
+    __shared__ uint16_t s_off[PAIR ? 4 : 1][3][64];
     // Causal work grows with the query block.  Unsplit launches: workgroups
     // are dispatched in linear order and the second half of the grid lands
     // beside the first half on the CUs, so kv heads 0-3 take the query blocks
@@ -398,11 +402,12 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
     const int ks_clamp = ((kend - 1) / 4) * 4;        // last 16-byte chunk holding a visible key
     // Per-lane byte offsets of the DMA sources relative to the tile's first key
     // (the kv head folded in); the tile base itself is wave-uniform.
-    // PAIR: these offsets (and the Q addresses of load_q below) are formed at
-    // each use from an opaque copy of the lane id; the compiler would
-    // otherwise form them once and keep them live across the tile loop, at a
-    // register budget that leaves no room for them (spills, and every reload
-    // waits for the tile DMA in flight).
+    // PAIR: these offsets are re-read from LDS at each issue (issue_to), and
+    // what is still formed from the lane id (the key-scale offset, the clamped
+    // rows of a block's last tile, the Q addresses of load_q below) from an
+    // opaque copy of it; the compiler would otherwise form them once and keep
+    // them live across the tile loop, at a register budget that leaves no room
+    // for them (spills, and every reload waits for the tile DMA in flight).
     auto dma_lane = [&]() -> int {
         if constexpr (PAIR) {
             int l;
@@ -427,9 +432,25 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         const uint32_t sb = lds_st + (uint32_t) (si * sizeof(PfStage));
         const int kb0 = kt * PF_BK;
         const int ln = dma_lane();
-        const uint32_t so_k8 = so_k8_of(ln), so_ks = so_ks_of(ln);
-        const uint32_t so_kh[2] = {so_kv_of(ln, 0, false), so_kv_of(ln, 1, false)};
-        const uint32_t so_v[2] = {so_kv_of(ln, 0, true), so_kv_of(ln, 1, true)};
+        uint32_t so_k8, so_kh[2], so_v[2];
+        const uint32_t so_ks = so_ks_of(ln);
+        if constexpr (PAIR) {
+            // three LDS reads instead of forming five offsets (about 40 VALU
+            // instructions per issue; measured at C4 93.0 -> 89.5 us int8,
+            // 88.3 -> 86.7 us fp16); asm so that the compiler neither keeps
+            // them live across the tile loop nor counts them
+            uint32_t o0, o1, o2;
+            const uint32_t oa = lk_lds_addr(&s_off[hw][0][0]) + 2u * (uint32_t) ln;
+            asm volatile("ds_read_u16 %0, %3\n\tds_read_u16 %1, %3 offset:128\n\tds_read_u16 %2, %3 offset:256\n\t"
+                         "s_waitcnt lgkmcnt(0)" : "=&v"(o0), "=&v"(o1), "=&v"(o2) : "v"(oa) : "memory");
+            so_k8 = o0;
+            so_kh[0] = o1; so_kh[1] = (o1 + 8192u) ^ 64u;     // key group 1: 8 rows on, swizzle bit 2 flipped
+            so_v[0] = o2;  so_v[1] = o2 + 8192u;              // (the V swizzle repeats every 8 rows)
+        } else {
+            so_k8 = so_k8_of(ln);
+            so_kh[0] = so_kv_of(ln, 0, false); so_kh[1] = so_kv_of(ln, 1, false);
+            so_v[0] = so_kv_of(ln, 0, true); so_v[1] = so_kv_of(ln, 1, true);
+        }
         if (kb0 + PF_BK <= kend) {                        // whole tile visible: no clamping
             const int8_t * kb8 = k8 + (size_t) kb0 * LK_KV_ROW;
             const _Float16 * kbh = kc + (size_t) kb0 * LK_KV_ROW;
@@ -514,6 +535,12 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     };
     if constexpr (PAIR) {
+        if (grp == 0) {                               // group B's wave of the same head reads them too
+            s_off[hw][0][lane] = (uint16_t) so_k8_of(lane);
+            s_off[hw][1][lane] = (uint16_t) so_kv_of(lane, 0, false);
+            s_off[hw][2][lane] = (uint16_t) so_kv_of(lane, 0, true);
+        }
+        __syncthreads();                              // before any wave's first issue
         if (tid < 2) { s_gbar[tid] = 0u; s_gbad[tid] = 0u; }
         // (the workgroup barrier after the Q prologue below orders this
         // before every group barrier)
