@@ -1316,15 +1316,16 @@ static int pf_part_release(hipStream_t st, int dev) {
 }
 
 static int pf_slots_per_device() {
-    static int cus[64] = {};
+    // looked up once per device; threads that race here store the same value
+    static std::atomic<int> cus[64] = {};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 512;
-    if (!cus[dev]) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
+    int c = cus[dev].load(std::memory_order_relaxed);
+    if (!c) {
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev].store(c, std::memory_order_relaxed);
     }
-    return 2 * cus[dev];                                  // two attention workgroups per CU
+    return 2 * c;                                         // two attention workgroups per CU
 }
 
 // The work list of this chunk: n_items = 0 for an unsplit launch.
