@@ -636,13 +636,15 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 // exact tiles' score in units of 1/sq: (sum*log2e - qc) / sq as one fma
                 const float isq = 1.0f / sq[qb];
                 const float qc = ok ? cv : 0.0f;
-                exa[qb] = LK_LOG2E_F * isq;
-                exb[qb] = -qc * isq;
+                // PAIR forms the exponent argument in the score step: an exact
+                // tile's is sum*log2e - qc - moff, one fma
+                exa[qb] = PAIR ? LK_LOG2E_F : LK_LOG2E_F * isq;
+                exb[qb] = PAIR ? -qc : -qc * isq;
             } else {
                 // every tile exact: scores stay the raw fp32 sums (natural-log
                 // units) and log2(e) is the exponent's scale, so the exponent
                 // argument is one fma of the raw sum
-                qf8[qb] = zi; sq[qb] = LK_LOG2E_F; exa[qb] = 1.0f; exb[qb] = 0.0f;
+                qf8[qb] = zi; sq[qb] = LK_LOG2E_F; exa[qb] = PAIR ? LK_LOG2E_F : 1.0f; exb[qb] = 0.0f;
             }
         }
         if (fill_s_q && !fuse_q) fill_sq(qv16);
@@ -733,7 +735,17 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 #pragma unroll
         for (int hq = 0; hq < 2; ++hq) {
             const bool ex = (md == PF_EXACT) || (md == PF_MIXED && hq == 0);
+            // x: unpaired launches, the score in units of 1/sq; PAIR, the
+            // exponent argument x*sq - moff itself (one fma per score on exact
+            // tiles instead of two), taken against offset 0 on a part's first
+            // tile (every query at -inf: wave-uniform), whose offset is then set
+            // from the tile max
             float x[4][2][4];               // [key block][query block 2hq+j][i]: key kb0+16kb+4g+i
+            const bool first = PAIR &&
+                __builtin_amdgcn_readfirstlane(__float_as_int(mst[2 * hq])) == __float_as_int(-INFINITY);
+            float mo2[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) mo2[j] = first ? 0.0f : mst[2 * hq + j];
             if (ex) {
                 lk_h8 qa[2][2];
 #pragma unroll
@@ -754,7 +766,8 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qa[j][1], c, 0, 0, 0);
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
-                            x[kb][j][i] = INT8 ? fmaf(c[i], exa[qb], exb[qb]) : c[i];
+                            x[kb][j][i] = PAIR ? fmaf(c[i], exa[qb], exb[qb] - mo2[j])
+                                               : INT8 ? fmaf(c[i], exa[qb], exb[qb]) : c[i];
                     }
                 }
             } else {
@@ -767,7 +780,10 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                     for (int j = 0; j < 2; ++j) {
                         const lk_f4 c = lk_mfma_qk8_magic(ka[kb], qf8[2 * hq + j]);
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) x[kb][j][i] = fmaf(c[i], sk[kb][i], skb[kb][i]);
+                        for (int i = 0; i < 4; ++i) {
+                            const float xs = fmaf(c[i], sk[kb][i], skb[kb][i]);
+                            x[kb][j][i] = PAIR ? fmaf(xs, sq[2 * hq + j], -mo2[j]) : xs;
+                        }
                     }
             }
             if (msk) {
@@ -792,14 +808,24 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int qb = 2 * hq + j;
-                    const float mo = moff(qb);
+                    if constexpr (PAIR) {
 #pragma unroll
-                    for (int kk = 0; kk < 2; ++kk)
+                        for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -mo));
-                            pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -mo));
-                        }
+                            for (int i = 0; i < 4; ++i) {
+                                pb[qb][kk][i]     = (_Float16) lk_exp2(x[2 * kk][j][i]);
+                                pb[qb][kk][4 + i] = (_Float16) lk_exp2(x[2 * kk + 1][j][i]);
+                            }
+                    } else {
+                        const float mo = moff(qb);
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -mo));
+                                pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -mo));
+                            }
+                    }
                 }
             };
             auto row_max = [&](int j) -> float {
@@ -811,12 +837,19 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                 return lk_xrow_max(v);                         // the 4 lane groups of this query
             };
             if constexpr (PAIR) {
-                // a part's first tile (every query at -inf: wave-uniform): the
-                // offset from the exact tile max before any p is formed (every
-                // query sees a key in it, so the max is finite)
-                if (__builtin_amdgcn_readfirstlane(__float_as_int(mst[2 * hq])) == __float_as_int(-INFINITY)) {
+                // a part's first tile: the offset from the exact tile max before
+                // any p is formed (every query sees a key in it, so the max is
+                // finite), and the arguments taken against it
+                if (first) {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) mst[2 * hq + j] = fmaf(row_max(j), sq[2 * hq + j], PF_P_BIAS);
+                    for (int j = 0; j < 2; ++j) {
+                        const float mn = row_max(j) + PF_P_BIAS;
+                        mst[2 * hq + j] = mn;
+#pragma unroll
+                        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) x[kb][j][i] -= mn;
+                    }
                 }
             }
             // Wave priorities by phase: exponent pass 2, int8 Q.K^T and the
@@ -862,22 +895,23 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                     for (int j = 0; j < 2; ++j) {
                         const int qb = 2 * hq + j;
                         if constexpr (PAIR) {
-                            // the offset of the queries past the limit moves to
-                            // their max + PF_P_BIAS; their p are formed again
-                            const float am = row_max(j) * sq[qb];
-                            const bool need = am - mst[qb] > PF_P_BIG - 1.0f;
+                            // the offset of the queries past the limit moves up
+                            // by dm, to their max + PF_P_BIAS (x is already
+                            // relative to the offset); their p are formed again
+                            const float am = row_max(j);
+                            const bool need = am > PF_P_BIG - 1.0f;
                             if (__ballot(need)) {
-                                const float mn = need ? am + PF_P_BIAS : mst[qb];
-                                const float alpha = need ? lk_exp2(mst[qb] - mn) : 1.0f;
-                                mst[qb] = mn;
+                                const float dm = need ? am + PF_P_BIAS : 0.0f;
+                                const float alpha = need ? lk_exp2(-dm) : 1.0f;
+                                mst[qb] += dm;
 #pragma unroll
                                 for (int db = 0; db < 5; ++db) acc[db][qb] *= alpha;
 #pragma unroll
                                 for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
                                     for (int i = 0; i < 4; ++i) {
-                                        pb[qb][kk][i]     = (_Float16) lk_exp2(fmaf(x[2 * kk][j][i], sq[qb], -mst[qb]));
-                                        pb[qb][kk][4 + i] = (_Float16) lk_exp2(fmaf(x[2 * kk + 1][j][i], sq[qb], -mst[qb]));
+                                        pb[qb][kk][i]     = (_Float16) lk_exp2(x[2 * kk][j][i] - dm);
+                                        pb[qb][kk][4 + i] = (_Float16) lk_exp2(x[2 * kk + 1][j][i] - dm);
                                     }
                             }
                         } else {
