@@ -716,15 +716,19 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
         lk_i4 ka[4];                        // int8 K fragments (key row 16kb+col)
         lk_f4 sk[4], skb[4];                // scales (keys 16kb+4g+i), 22-bit, and -PF_MAGIC times them
         if (md != PF_EXACT) {
-            // the scale pair of the tile's 64 keys, one key per lane, through
-            // this wave's own LDS rows (LDS accesses of a wave complete in order)
-            const float s22 = lk_pf_ks22(S.ks[lane]);
+            // the int8 K fragments first (LDS accesses of a wave complete in
+            // order: the MFMAs then wait for one LDS round trip, not for the
+            // scale staging behind it), then the scale pair of the tile's 64
+            // keys, one key per lane, through this wave's own LDS rows
+            const float ks_l = S.ks[lane];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) ka[kb] = *(const lk_i4 *) (S.k8 + o_k8 + 1024 * kb);
+            const float s22 = lk_pf_ks22(ks_l);
             s_kp[w][lane] = s22;
             s_kp[w][PF_BK + lane] = s22 * -PF_MAGIC;
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) {
-                ka[kb] = *(const lk_i4 *) (S.k8 + o_k8 + 1024 * kb);
                 sk[kb] = *(const lk_f4 *) (&s_kp[w][16 * kb + 4 * g]);
                 skb[kb] = *(const lk_f4 *) (&s_kp[w][PF_BK + 16 * kb + 4 * g]);
             }
