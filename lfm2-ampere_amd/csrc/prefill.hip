@@ -758,10 +758,21 @@ lk_k_pf_attn(const int8_t * __restrict__ q8, const float * __restrict__ qsc,
                     qa[j][0] = *(const lk_h8 *) qrow;
                     qa[j][1] = *(const lk_h8 *) (qrow + 64);
                 }
+                // PAIR: all eight K fragments in flight before the first MFMA
+                // (C4 1.5% faster; in the unpaired kernel, deep chunks 0.6%
+                // slower, so there each key block's pair is read at its use)
+                lk_h8 kf[4][2];
+                if constexpr (PAIR) {
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb) {
+                        kf[kb][0] = *(const lk_h8 *) (S.kh + o_kh0 + 2048 * kb);
+                        kf[kb][1] = *(const lk_h8 *) (S.kh + o_kh1 + 2048 * kb);
+                    }
+                }
 #pragma unroll
                 for (int kb = 0; kb < 4; ++kb) {
-                    const lk_h8 k0 = *(const lk_h8 *) (S.kh + o_kh0 + 2048 * kb);
-                    const lk_h8 k1 = *(const lk_h8 *) (S.kh + o_kh1 + 2048 * kb);
+                    const lk_h8 k0 = PAIR ? kf[kb][0] : *(const lk_h8 *) (S.kh + o_kh0 + 2048 * kb);
+                    const lk_h8 k1 = PAIR ? kf[kb][1] : *(const lk_h8 *) (S.kh + o_kh1 + 2048 * kb);
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
                         const int qb = 2 * hq + j;
