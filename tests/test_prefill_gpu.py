@@ -290,6 +290,58 @@ def test_attn_pair(lk, oracle, m, P, near):
     assert np.array_equal(host(aqs), qso) and np.array_equal(host(asc).view(np.uint32), sco.view(np.uint32))
 
 
+# ---- the rescale path: scores that climb past the running offset in every tile -----------------
+RESCALE_CASES = [(600, 0, 96), (256, 300, 1024), (333, 100, 0)]
+
+
+def _climbing_case(m, P, seed=7):
+    """Keys along one direction u per kv head with a length growing by 1/8 per
+    position, queries along the same u (length 2): the score q.k climbs by
+    about 16 natural-log units (23 log2 units) per 64-key tile, so every tile
+    raises some query's running max past the 2^15 limit of p and takes the
+    rescale path; the softmax stays well conditioned (consecutive keys differ
+    by 0.25 in score, so about four keys carry each row)."""
+    rng = np.random.default_rng(seed)
+    S = P + m
+    u = rng.standard_normal((8, 64))
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    beta = 0.5 + np.arange(S) * 0.125
+    K = beta[:, None, None] * u[None] + 0.05 * rng.standard_normal((S, 8, 64))
+    V = rng.standard_normal((S, 8, 64))
+    Q = 2.0 * np.repeat(u, 4, axis=0)[None] + 0.05 * rng.standard_normal((m, 32, 64))
+    f16 = lambda a: np.ascontiguousarray(a.astype(np.float16)).view(np.uint16).reshape(-1)
+    return f16(K), f16(V), f16(Q)
+
+
+@pytest.mark.parametrize("m,P,near", RESCALE_CASES, ids=[f"m{c[0]}_P{c[1]}_n{c[2]}" for c in RESCALE_CASES])
+def test_attn_rescale_every_tile(lk, oracle, m, P, near):
+    """The offset raise (a score more than 20 log2 units past the running
+    offset) in every key tile, through the paired, unpaired and split
+    launches: the fp16 kernel against float64, the int8 kernel against the
+    float64 restatement of its algorithm, both within 2e-3 relative."""
+    K, V, Q = _climbing_case(m, P)
+    sink = int(near > 0)
+    note(f"pf rescale every tile m={m} P={P} near={near}")
+    d = _Dev(lk, K, V, Q, m, P, False)
+    ref = oracle.pf_ref(Q, m, P, K, V)
+    ref8 = oracle.pf_ref8(host(d.q8), host(d.qsc), host(d.qcs), Q, m, P, host(d.k8), host(d.ksc),
+                          d.kstride, K, V, near, sink)
+    forms = {}
+    try:
+        for name, pair, split in (("paired", 1, 0), ("unpaired", -1, 0), ("split", -1, 1)):
+            lk.pf_pair_override(pair)
+            lk.pf_split_override(split)
+            forms[name] = (d.attn8(lk, near, sink), d.attn16(lk))
+    finally:
+        lk.pf_pair_override(0)
+        lk.pf_split_override(0)
+    for name, (o8, o16) in forms.items():
+        r8, r16 = oracle.rel_err(o8, ref8), oracle.rel_err(o16, ref)
+        note(f"  {name}: int8 rel {r8:.3e}, fp16 rel {r16:.3e}")
+        assert np.isfinite(o8).all() and np.isfinite(o16).all(), name
+        assert r8 <= 2e-3 and r16 <= 2e-3, name
+
+
 # ---- the automatic (cost-model) split plan ------------------------------------------------------
 AUTO_CASES = [(1000, 0, 256), (777, 0, 1024), (1500, 300, 96), (2048, 777, 1024), (4096, 4096, 1024),
               (512, 8000, 1024), (300, 20000, 256)]          # short chunks deep in a prompt: few blocks
