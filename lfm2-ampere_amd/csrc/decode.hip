@@ -8,10 +8,14 @@
 // for the 32 query heads, K/V of kv head h/4 in the fp16 cache [pos][8][64].
 //
 // MI355X design (not a translation of the reference's warp-level loops):
-//   * grid of LK_ATTN_SPLIT 8-wave workgroups, one per contiguous slice of
-//     positions covering ALL 8 kv heads: whole 1 KB cache rows are streamed
-//     once into LDS by LDS DMA (algorithmic traffic: seq x 2 KB per layer);
-//     wave w then serves kv head w and its 4 query heads;
+//   * grid of LK_ATTN_SPLIT 8-wave workgroups, one per slice covering ALL 8
+//     kv heads; the reference's slice count, but a slice is the set of tiles
+//     of LK_DEC_TILE positions congruent to it modulo the slice count, not a
+//     contiguous range (all workgroups then stream one moving front of the
+//     cache: measured about 6% faster than contiguous shares at 32k-131k);
+//     whole 1 KB cache rows are streamed once into LDS by LDS DMA
+//     (algorithmic traffic: seq x 2 KB per layer); wave w then serves kv
+//     head w and its 4 query heads;
 //   * S^T = K . q^T on the matrix cores (v_mfma_f32_16x16x32_f16, keys as the
 //     A operand).  q is fp32 in the interface, so it is split q = hi + lo into
 //     two fp16 halves (22 significant bits; fp16 x fp16 products are exact in
@@ -34,7 +38,8 @@ __device__ __forceinline__ void lk_split_h(float x, _Float16 & hi, _Float16 & lo
 }
 
 // ---- decode split kernel ------------------------------------------------------
-// The workgroup of slice sp covers ALL 8 kv heads of positions [t0, t1): cache
+// The workgroup of slice sp covers ALL 8 kv heads of the tiles sp, sp + ns,
+// sp + 2 ns, ... (tile T = positions 16T .. 16T+15, below seq): cache
 // rows (one position = 8 heads x 64 dims = 1 KB of K, same of V) are fetched
 // whole, 64 lanes x 16 contiguous bytes per instruction, straight into LDS
 // (global_load_lds_dwordx4, no staging registers), into a ring of LK_DEC_NBUF
@@ -138,25 +143,21 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     const int seq = *d_pos + 1;
     int ns, chunk;
     lk_attn_slices(seq, ns, chunk);
+    (void) chunk;
     const int sp = blockIdx.x;
-    const int t0 = sp * chunk;
-    const int t1 = (t0 + chunk < seq) ? (t0 + chunk) : seq;
-    // Block-uniform early out before any barrier: a dead slice writes the
-    // neutral record (m = -inf, l = 0, acc = 0) of each query head, so every
-    // slot the combine reads is valid without it knowing seq.
-    if (t0 >= t1) {
-        for (int i = threadIdx.x; i < LK_N_HEADS * 16; i += LK_DEC_THREADS) {
-            const int h = i >> 4, k = i & 15;
-            *(lk_f4 *) (part + lk_part_acc(h, k >> 2, sp) + 4 * (k & 3)) = (lk_f4){ 0.0f, 0.0f, 0.0f, 0.0f };
-        }
-        if (threadIdx.x < LK_N_HEADS)
-            *(float2 *) (part + lk_part_ml(threadIdx.x, sp)) = make_float2(-INFINITY, 0.0f);
-        return;
-    }
-    const int n = t1 - t0;
-    const int ntile = (n + LK_DEC_TILE - 1) / LK_DEC_TILE;
+    // Slice sp holds tiles T = sp + ns * it, it < ntile, of the nt tiles that
+    // cover [0, seq): slices differ by at most one tile.
+    const int nt = (seq + LK_DEC_TILE - 1) / LK_DEC_TILE;
+    const int ntile = (sp < ns && sp < nt) ? (nt - sp + ns - 1) / ns : 0;
+    // A slice with no tiles (ntile = 0: sp >= nt or sp >= ns) takes the same
+    // path with an empty tile loop, so its record is the neutral one (m =
+    // -inf, l = 0, acc = 0) and every slot the combine reads is valid without
+    // it knowing seq.  There is no early return: the untracked loads above
+    // are in flight until the wait below, and code on a separate path would
+    // be free to reuse their registers (a store address formed in one of
+    // them would be overwritten by the arriving data).
     const int pos = seq - 1;
-    const bool own_pos = FUSED && t1 == seq;               // this slice holds position pos
+    const bool own_pos = FUSED && (nt - 1) % ns == sp;     // this slice holds position pos (its last tile)
     if constexpr (FUSED) {          // loaded by every workgroup: see the wait below
         const float * kp = pr.k_src + w * LK_HEAD_DIM + 8 * g;
         const float * vp = pr.v_src + w * LK_HEAD_DIM + 8 * g;
@@ -171,17 +172,26 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
     }
 
     // ---- fetch: wave w brings rows w, w+8, ... of each tile (K rows first) ----
-    const char * kg = (const char *) (kc + (size_t) t0 * LK_KV_ROW) + 16 * lane;
-    const char * vg = (const char *) (vc + (size_t) t0 * LK_KV_ROW) + 16 * lane;
+    const char * kg = (const char *) kc + 16 * lane;
+    const char * vg = (const char *) vc + 16 * lane;
     const uint32_t lds0 = lk_lds_addr(&s_tile[0][0]);
+    // first position of the slice's tile it
+    auto tile_pos = [&](int it) -> int { return (sp + ns * it) * LK_DEC_TILE; };
+    const int clamp_row = ntile > 0 ? sp * LK_DEC_TILE : 0;
     auto fetch = [&](int it) {
         const uint32_t base = lds0 + (uint32_t) ((it % LK_DEC_NBUF) * LK_DEC_TILEB);
+        const int p0 = tile_pos(it);
 #pragma unroll
         for (int i = 0; i < RPW; ++i) {
             const int row = w + 8 * i;                         // 0 .. 2*TILE-1
             const bool isv = row >= LK_DEC_TILE;
-            const int tt = it * LK_DEC_TILE + (isv ? row - LK_DEC_TILE : row);
-            const size_t o = (size_t) (tt < n ? tt : 0) * (LK_KV_ROW * 2);   // clamp: t0 is in range
+            const int tp = p0 + (isv ? row - LK_DEC_TILE : row);
+            // clamp: rows past seq and whole tiles past the slice's last fetch
+            // the slice's first row (in range, and a different row in every
+            // workgroup: a row shared by all of them would put every clamped
+            // fetch on one L2 channel), all tiles of an empty slice row 0;
+            // they are masked or land in buffers no tile of the slice uses
+            const size_t o = (size_t) (it < ntile && tp < seq ? tp : clamp_row) * (LK_KV_ROW * 2);
             lk_dma16((isv ? vg : kg) + o, base + (uint32_t) (row * LK_DEC_ROWB));
         }
     };
@@ -341,10 +351,10 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
             c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qbh[1], c, 0, 0, 0);
             c = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qbl[1], c, 0, 0, 0);
 #endif
-            const int t0g = it * LK_DEC_TILE + 16 * gi + 4 * g;
+            const int t0g = tile_pos(it) + 16 * gi + 4 * g;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                x[gi][r] = (t0g + r < n) ? c[r] * SC : -INFINITY;
+                x[gi][r] = (t0g + r < seq) ? c[r] * SC : -INFINITY;
                 mloc = fmaxf(mloc, x[gi][r]);
             }
         }
@@ -396,7 +406,7 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
         if (own_pos && it == ntile - 1 && col == 0) {
             // the new row, as the cache now holds it (the tile's copy may predate
             // the store above); wave w alone reads kv head w's bytes of a row
-            const int rt = pos - t0 - it * LK_DEC_TILE;
+            const int rt = pos - tile_pos(it);
             unsigned char * b = s_tile[it % LK_DEC_NBUF] + w * 128 + 16 * g;
             *(lk_h8 *) (b + rt * LK_DEC_ROWB) = kv_h[0];
             *(lk_h8 *) (b + rt * LK_DEC_ROWB + 64) = kv_h[1];
@@ -405,6 +415,10 @@ lk_k_attn_split(const float * __restrict__ q, const _Float16 * kc,
         }
         consume(s_tile[it % LK_DEC_NBUF], it);
     }
+    // every tile DMA has landed before the workgroup ends (an empty slice
+    // issued its first D tiles and never waited for them; for the others the
+    // last wait_tile already waited for all)
+    lk_wait_vm<0>();
 
     // Partial record of query head 4w + c, written by the lanes of columns
     // c = 0..3: O^T rows 16db + 4g + r; the sum of p is in every row of accl.
@@ -454,8 +468,8 @@ __device__ __forceinline__ void lk_quant_q8_1_half(float x, lk_block_q8_1 * __re
 // Combine: grid (32 query heads, 2 halves of the 64 dims), 256 threads;
 // workgroup (head, half) produces 32 output dims, wave w owns dims
 // 32*half + 8w .. +7 over all slots, lane l the slots l, l+64, l+128, l+192.
-// Slices s with s*chunk >= seq hold no tokens (reference kernels.cu:1573-1584);
-// their workgroups wrote the neutral record (m = -inf, l = 0, acc = 0), whose
+// Slices that hold no tile (the reference's empty slices, kernels.cu:1573-1584,
+// hold no tokens either) wrote the neutral record (m = -inf, l = 0, acc = 0), whose
 // weight 2^(-inf - M) is exactly 0, so every slot is merged and d_pos is not
 // read: all of a lane's loads go out at once, one memory round trip.  The max
 // M is exact, the slot weights are 2^(m_s - M).  Every sum runs in a fixed

@@ -155,11 +155,12 @@ def test_null_outputs_and_q8_only(lk, oracle):
     assert torch.equal(y1, y2)
 
 
-@pytest.mark.parametrize("seq", [1, 9, 17, 1025, 1031, 4100])
+@pytest.mark.parametrize("seq", [1, 9, 17, 100, 112, 113, 1025, 1031, 4100])
 def test_dead_slices_write_neutral_records(lk, oracle, seq):
-    """Lengths whose slice plan leaves empty slices (seq / ceil(seq / ns) < ns,
-    and every slot past ns): the partial buffer starts as NaN everywhere, the
-    combine merges all slots, and the result is the float64 reference's."""
+    """Slots whose slice holds no tile (fewer 16-position tiles than slices:
+    seq <= 112, and every slot past the slice count) and lengths around that
+    edge: the partial buffer starts as NaN everywhere, the combine merges all
+    slots, and the result is the float64 reference's."""
     rng = np.random.default_rng(seq)
     q = rng.standard_normal((32, 64)).astype(np.float32)
     kc = rng.standard_normal((seq, 8, 64)).astype(np.float16)

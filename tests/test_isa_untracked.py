@@ -4,8 +4,10 @@ them with one `s_waitcnt vmcnt(D*RPW)` that names their registers.  The
 compiler does not know those registers are pending until that wait: any
 instruction that touches them in between would read or clobber data still in
 flight.  This CPU test compiles decode.hip for gfx950 (the library's flags) and
-checks the generated assembly, in program order, for such an instruction, and
-that the first vector-memory wait after the loads leaves the tile DMAs in flight.
+checks the generated assembly along every control-flow path (branches
+followed, so the early return of a slice with no positions is covered as well
+as the tile loop) for such an instruction, and that the first vector-memory
+wait after the loads leaves the tile DMAs in flight.
 """
 import os
 import re
@@ -31,6 +33,66 @@ def _vregs(text):
     return out
 
 
+def _check_paths(name, body):
+    """Dataflow over the kernel's instructions: the set of registers of
+    untracked loads still in flight at each instruction, joined over every
+    path that reaches it; any instruction other than a vector-memory wait that
+    names one of them is a hazard.  Returns (number of untracked loads, vmcnt
+    of the first wait that retires them)."""
+    ins, labels = [], {}
+    in_asm = False
+    for l in body:
+        if l.startswith(";;#ASMSTART"):
+            in_asm = True
+            continue
+        if l.startswith(";;#ASMEND"):
+            in_asm = False
+            continue
+        m = re.match(r"^(\.?[A-Za-z_][\w.$]*):", l)
+        if m:
+            labels[m.group(1)] = len(ins)
+            continue
+        if l.startswith(";") or not l or (l.startswith(".") and not in_asm):
+            continue
+        ins.append((l.split(";")[0].strip(), in_asm))
+    loads = sum(1 for t, a in ins if a and t.startswith("global_load_dwordx4") and "lds" not in t)
+    state = [None] * (len(ins) + 1)
+    state[0] = frozenset()
+    work, first_wait = [0], None
+    while work:
+        k = work.pop()
+        if k >= len(ins):
+            continue
+        t, a = ins[k]
+        pend = state[k]
+        op = t.split()[0]
+        if a and op == "global_load_dwordx4" and "lds" not in t:
+            out = pend | _vregs(t.split(None, 1)[1].split(",")[0])
+        elif "vmcnt(" in t:
+            if pend and first_wait is None:
+                first_wait = int(re.search(r"vmcnt\((\d+)\)", t).group(1))
+            out = frozenset()
+        else:
+            hit = _vregs(t) & pend
+            assert not hit, "%s: %s touches registers of loads in flight %s" % (name, t, sorted(hit))
+            out = pend
+        succ = []
+        if op == "s_endpgm":
+            succ = []
+        elif op == "s_branch":
+            succ = [labels[t.split()[1]]]
+        elif op.startswith("s_cbranch"):
+            succ = [k + 1, labels[t.split()[1]]]
+        else:
+            succ = [k + 1]
+        for j in succ:
+            new = out if state[j] is None else (state[j] | out)
+            if state[j] is None or new != state[j]:
+                state[j] = new
+                work.append(j)
+    return loads, first_wait
+
+
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
 def test_untracked_loads_untouched_until_their_wait(tmp_path):
     asm = tmp_path / "decode.s"
@@ -42,27 +104,7 @@ def test_untracked_loads_untouched_until_their_wait(tmp_path):
         name = "_Z15lk_k_attn_splitILb%dE" % fused
         i = txt.index("\n" + name) + 1
         body = [l.strip() for l in txt[i:txt.index(".Lfunc_end", i)].split("\n")]
-        pending, in_asm, loads, first_wait = set(), False, 0, None
-        for k, l in enumerate(body):
-            if l.startswith(";;#ASMSTART"):
-                in_asm = True
-                continue
-            if l.startswith(";;#ASMEND"):
-                in_asm = False
-                continue
-            if in_asm and l.startswith("global_load_dwordx4") and "lds" not in l:
-                pending |= _vregs(l.split()[1])
-                loads += 1
-                continue
-            if "vmcnt(" in l:
-                if pending and first_wait is None:
-                    first_wait = int(re.search(r"vmcnt\((\d+)\)", l).group(1))
-                pending = set()
-                continue
-            if l.startswith((".", ";")) or not l:
-                continue
-            hit = _vregs(l) & pending
-            assert not hit, "%s line %d touches pending registers %s: %s" % (name, k, sorted(hit), l)
+        loads, first_wait = _check_paths(name, body)
         assert loads == (20 if fused else 4), (name, loads)
         # D = 3 tiles of RPW = 4 rows per wave stay in flight
         assert first_wait == 12, (name, first_wait)
