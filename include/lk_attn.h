@@ -74,9 +74,11 @@ const char * lk_last_error(void);
 
 /* Replaces k_attn_split (reference kernels.cuh:647-649, kernels.cu:1303-1556).
  * Grid (split_cap) of 8-wave workgroups, each over all 8 kv heads of one
- * contiguous slice of positions; workgroups past the live slice count write
- * the neutral record (m = -inf, l = 0, acc = 0) of their slot and exit, so
- * every one of the split_cap slots of part is valid afterwards. */
+ * slice: the slice count is the reference's rule (lk_attn_slices), and slice
+ * s holds the 16-position tiles s, s + ns, s + 2ns, ... of [0, seq).
+ * Workgroups whose slice holds no tile write the neutral record (m = -inf,
+ * l = 0, acc = 0) of their slot, so every one of the split_cap slots of part
+ * is valid afterwards. */
 int lk_attn_split(const float * q, const void * kc, const void * vc,
                   const int * d_pos, float * part, void * stream);
 
