@@ -176,6 +176,27 @@ def test_dead_slices_write_neutral_records(lk, oracle, seq):
     assert abs_err(o, ref) <= 1e-3
 
 
+@pytest.mark.parametrize("seq", [127, 128, 129, 4095, 4096, 4097, 4111, 4112, 4113, 8193, 12345])
+def test_slice_and_tile_edges(lk, oracle, seq):
+    """Lengths at the edges of the slice layout: the slice count reaching 8 and
+    256, a last tile of 1, 15 and 16 positions, slices holding one or two
+    tiles (at 4097 slice 0 holds tiles 0 and 256): split + combine against
+    the float64 reference, and repeat bit-identity."""
+    rng = np.random.default_rng(seq + 7)
+    q = rng.standard_normal((32, 64)).astype(np.float32)
+    kc = rng.standard_normal((seq, 8, 64)).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal((seq, 8, 64)).astype(np.float16).view(np.uint16)
+    note(f"decode slice/tile edges seq={seq}")
+    qd, kd, vd = dev(q), dev_h(kc), dev_h(vc)
+    o1, _ = _run_decode(lk, qd, kd, vd, seq)
+    o2, _ = _run_decode(lk, qd, kd, vd, seq)
+    ref = oracle.decode_ref(q, kc, vc, seq)
+    o = host(o1)
+    assert np.isfinite(o).all()
+    assert abs_err(o, ref) <= 1e-3 and oracle.rel_err(o, ref) <= 2e-3
+    assert torch.equal(o1.view(torch.int32), o2.view(torch.int32))
+
+
 def test_serial_beyond_limit_writes_nothing(lk):
     seq = lk.DECODE_MAX_SEQ + 1
     q = torch.randn(32, 64, device="cuda")
@@ -254,7 +275,7 @@ def test_config_c3_graph(lk, oracle):
     _check_config(lk, oracle, "C3", 10, [0, 9])
 
 
-@pytest.mark.parametrize("P0,steps", [(1000, 5), (0, 3), (14, 4), (2047, 3)])
+@pytest.mark.parametrize("P0,steps", [(1000, 5), (0, 3), (14, 4), (2047, 3), (4094, 4)])
 def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle, P0, steps):
     """The decode step graph (per layer: qk norm + RoPE + cache append folded
     into the split, combine; d_pos += 1 in the last combine) replayed n times =
@@ -262,7 +283,9 @@ def test_decode_step_graph_runs_steps_like_the_oracle(lk, oracle, P0, steps):
     rows, d_pos and every layer's output against the oracle, and the replay
     bit-identical to the same kernels called eagerly."""
     rng = np.random.default_rng(61)
-    layers, cap = 3, 2048 + 64
+    # from 4094 the slice count reaches 256 and the new row moves into the
+    # second tile of slice 0
+    layers, cap = 3, max(2048, P0 + steps) + 64
     note(f"decode step graph: {layers} layers, {steps} steps from position {P0}")
     Ls, host_in = [], []
     for i in range(layers):
